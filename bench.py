@@ -1,0 +1,222 @@
+"""Benchmark of the GLM-5.2 MoE FFN block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--tokens 1,256,8192]
+
+A step is one pass of the whole block (ResAdd+RMSNorm -> router -> top-8 -> dispatch ->
+routed w13+SwiGLU / shared w13+SwiGLU -> routed w2 / shared w2 -> merge+ResAdd) over one
+batch of T synthetic tokens, with the real 256-expert weight set (19.3 GB) resident.
+The headline `value` is microseconds per block at T = 1 (configuration 1); T = 256 and
+8192 are reported under `per_T`.  Timing follows the reference's `bench_chain`
+(`glm52/common.py:73-122`): one cache flush (1 GiB, larger than the 256 MB Infinity
+Cache) before every step, never inside it, and HIP events around the step; decode
+steps replay a captured HIP graph.  The dominant kernel (routed w13 + SwiGLU) is also
+timed alone with events on its stream, for the `roofline` object.  The CPU baseline is
+the oracle's restatement of `glm52/reference.py`'s path (fp32 router, per-expert bf16
+`moe_mlp`, fp32 shared expert) on this host's cores at T = 1.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "MoE-layer µs at T=1/256/8192 + % of roofline (HBM GB/s or MFMA util)"
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tokens", default="1,256,8192",
+                    help="token counts; the first is the headline (configuration 1 is T=1)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--json-out", default="")
+    return ap.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(the block's sharding is a design note only); run with --gpus 1", flush=True)
+        return 2
+
+    import torch
+
+    from fusion_amd import roofline as RL
+    from fusion_amd.block import MoEBlock
+    from fusion_amd.kernels.moe_gateup import moe_gemm
+    from fusion_amd.problem import expert_weights, front_end
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    W = expert_weights(device=dev)
+    torch.cuda.synchronize()
+    log(f"weights ready in {time.time() - t0:.1f}s")
+    flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)  # 1 GiB
+
+    def flush():
+        flush_buf.zero_()
+
+    def timed(fn, steps, warmup):
+        for _ in range(warmup):
+            flush()
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        w0 = time.perf_counter()
+        for s, e in ev:
+            flush()
+            s.record()
+            fn()
+            e.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - w0
+        ms = [s.elapsed_time(e) for s, e in ev]
+        return ms, wall
+
+    tokens = [int(t) for t in args.tokens.split(",") if t]
+    per_T = {}
+    headline = None
+    for T in tokens:
+        bias = "zipf" if T == 8192 else "normal"
+        fe = front_end(T, bias=bias)
+        x, r = fe.x.to(dev), fe.r.to(dev)
+        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), W.w13, W.w2,
+                       W.w13s, W.w2s)
+        blk(x, r)
+        torch.cuda.synchronize()
+        n_e = int(torch.unique(blk.topi).numel())
+        use_graph = (not args.no_graph) and T <= 256
+        if use_graph:
+            blk.capture(x, r)
+            step = blk.replay
+        else:
+            step = lambda: blk(x, r)  # noqa: E731
+        ms, wall = timed(step, args.steps, args.warmup)
+        eager_ms = None
+        if use_graph:
+            eager_ms, _ = timed(lambda: blk(x, r), args.steps, args.warmup)
+
+        # dominant kernel alone: routed w13 + SwiGLU, events on its stream
+        R = T * 8
+
+        def w13():
+            moe_gemm(blk.y, 8, blk.w13, blk.act, None, blk.sti, blk.eids, blk.ntp, R, blk.I,
+                     blk.I, True, blk.cfg_r)
+
+        k_ms, _ = timed(w13, args.steps, 2)
+        kc = RL.kernel("w13", T, n_e)
+        k_us = statistics.mean(k_ms) * 1e3
+        roof_us = RL.block_roofline_us(T, n_e)
+        med_us = statistics.median(ms) * 1e3
+        rec = {
+            "us_per_block": round(med_us, 2),
+            "us_mean": round(statistics.mean(ms) * 1e3, 2),
+            "us_min": round(min(ms) * 1e3, 2),
+            "graph": use_graph,
+            "eager_us": round(statistics.median(eager_ms) * 1e3, 2) if eager_ms else None,
+            "wall_us_per_step_incl_flush": round(wall / args.steps * 1e6, 1),
+            "distinct_experts": n_e,
+            "block_roofline_us": round(roof_us, 1),
+            "block_roofline_frac": round(roof_us / med_us, 4),
+            "w13_us": round(k_us, 2),
+            "w13_GBps": round(kc.bytes / (k_us * 1e-6) / 1e9, 1),
+            "w13_TFLOPs": round(kc.flops / (k_us * 1e-6) / 1e12, 1),
+            "block_m": blk.bm,
+            "bias": bias,
+        }
+        per_T[str(T)] = rec
+        log(f"T={T}: {rec}")
+        if headline is None:
+            headline = (T, rec, kc, k_us, n_e)
+        del blk, x, r
+        torch.cuda.empty_cache()
+
+    T, rec, kc, k_us, n_e = headline
+    achieved = kc.bytes / (k_us * 1e-6) / 1e9
+    roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
+            "frac": round(achieved / 8000.0, 4), "traffic": None,
+            "kernel": "moe_gemm_stream_kernel<gated> (routed w13 + SwiGLU)",
+            "algorithmic_bytes": int(kc.bytes), "avg_us": round(k_us, 2)}
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(W, tokens[0], args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": rec["us_per_block"], "unit": "us", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(rec["us_per_block"] / 1e3, 5),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, random init)",
+        "config": {"workload": f"config1: full GLM-5.2 MoE FFN block, decode T={T}", "T": T,
+                   "experts": 256, "shared_experts": 1, "topk": 8, "H": 6144, "I": 2048,
+                   "weights_GB": 19.33, "graph_replay": rec["graph"]},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "per_T": per_T,
+    }
+    s = json.dumps(line)
+    print(s, flush=True)
+    if args.json_out:
+        Path(args.json_out).write_text(s + "\n")
+    return 0
+
+
+def cpu_baseline(W, T: int, seconds: float) -> dict:
+    """The oracle's restatement of the reference path at T tokens on the host cores."""
+    import torch
+
+    from fusion_amd.problem import front_end
+    from oracle import glm52_oracle as O
+
+    ncores = min(16, os.cpu_count() or 1)
+    torch.set_num_threads(ncores)
+    fe = front_end(T)
+    y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+    _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
+    experts = sorted(set(ti.view(-1).tolist()))
+    w13 = {e: W.w13[e].cpu() for e in experts}
+    w2 = {e: W.w2[e].cpu() for e in experts}
+    w13s, w2s = W.w13s.cpu(), W.w2s.cpu()
+
+    def block():
+        y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+        _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
+        routed = O.moe_mlp_rows(y, w13, w2, tw, ti, list(range(T))).to(torch.bfloat16).float()
+        s = O.shared_expert(y, w13s, w2s)
+        return (routed + h.float() + s).to(torch.bfloat16)
+
+    block()
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        block()
+        times.append(time.perf_counter() - t0)
+    return {"value": round(statistics.median(times) * 1e6, 1), "unit": "us", "cores": ncores,
+            "kind": "port",
+            "sample": f"{len(times)} full blocks at T={T} (configuration 1) over ~{seconds:.0f}s; "
+                      f"torch-CPU fp32 router + per-expert bf16 moe_mlp + fp32 shared expert, "
+                      f"median"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

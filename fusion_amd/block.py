@@ -1,0 +1,151 @@
+"""The GLM-5.2 MoE FFN block on one MI355X, composed from the drop-in launchers.
+
+Chain (`glm52/bench/bench_layer.py:395-481`, configuration `H_f3_f10` without o_proj, with
+the routing computed live instead of frozen, and the tail fused):
+
+    1. ResAdd+RMSNorm           h = bf16(x + r), y = RMSNorm(h)           add_rmsnorm
+    2. router logits            fp64-accumulated, fp32 out                router_gemm
+    3. sigmoid + biased top-8   ids, weights                              topk_only
+    4. dispatch/align           sglang layout, count kept on the device  moe_align
+    5. routed w13 + SwiGLU      act[8T, I]                                moe_gemm (gated)
+    6. shared w13 + SwiGLU      act_s[T, I]                               moe_gemm (gated, E=1)
+    7. routed w2 (weighted)     Y[8T, H] = w * (act . w2^T)               moe_gemm
+    8. shared w2                s[T, H]                                   moe_gemm (E=1)
+    9. merge + ResAdd           out = bf16(sum_k Y[t, k] + h + s)         block_merge
+
+Every buffer is allocated once in the constructor (destination passing, as the
+reference's `LayerProblem` does, `glm52/bench/bench_layer.py:316-346`); `forward` only
+launches kernels on torch's current stream and never syncs, so it can be captured in a
+HIP graph (`capture()`), which is how decode is meant to run.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import config as C
+from . import _lib
+from .dispatch import capacity, moe_align_block_size_into
+from .kernels import add_rmsnorm as KN
+from .kernels import norm_router as KR
+from .kernels.moe_gateup import moe_gemm
+
+BF16 = torch.bfloat16
+
+
+def default_block_m(T: int) -> int:
+    """Layout block size per regime: 16-row slices stream weights while each expert sees
+    a handful of rows; LDS-tiled blocks once rows per expert reach the tens."""
+    rows_per_expert = T * C.TOPK / C.E
+    if rows_per_expert <= 16:
+        return 16
+    if rows_per_expert <= 96:
+        return 64
+    return 128
+
+
+def shared_layout(T: int, block_m: int, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Layout of the single shared expert over T tokens: what
+    `moe_align_block_size(zeros(T, 1), BM, 1)` returns (`glm52/bench/bench_layer.py:384-388`),
+    padded to the worst-case capacity like the routed layout."""
+    cap = capacity(T, block_m, 1)
+    sti = torch.full((cap,), T, dtype=torch.int32)
+    sti[:T] = torch.arange(T, dtype=torch.int32)
+    total = ((T + block_m - 1) // block_m) * block_m
+    eids = torch.full((cap // block_m,), -1, dtype=torch.int32)
+    eids[: total // block_m] = 0
+    ntp = torch.tensor([total], dtype=torch.int32)
+    return sti.to(device), eids.to(device), ntp.to(device)
+
+
+class MoEBlock:
+    def __init__(self, T: int, w_norm, wgt, bias, w13, w2, w13s, w2s, block_m: int | None = None,
+                 shared_block_m: int | None = None, variant: str | None = None,
+                 eps: float = C.RMS_NORM_EPS, scale: float = C.ROUTED_SCALING_FACTOR):
+        _lib.require_gpu(w_norm, wgt, bias, w13, w2, w13s, w2s)
+        dev = w13.device
+        self.T = T
+        self.E, I2, self.H = w13.shape
+        self.I = I2 // 2
+        self.topk = C.TOPK
+        self.w_norm, self.wgt, self.bias = w_norm, wgt, bias
+        self.w13, self.w2 = w13, w2
+        self.w13s = w13s if w13s.dim() == 3 else w13s.unsqueeze(0)
+        self.w2s = w2s if w2s.dim() == 3 else w2s.unsqueeze(0)
+        self.eps, self.scale = eps, scale
+        self.bm = block_m or default_block_m(T)
+        self.sbm = shared_block_m or (16 if T <= 64 else (64 if T <= 1024 else 128))
+        self.variant = variant
+
+        H, I, E, R = self.H, self.I, self.E, T * self.topk
+        self.h = torch.empty(T, H, dtype=BF16, device=dev)
+        self.y = torch.empty(T, H, dtype=BF16, device=dev)
+        self.logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+        self.topw = torch.empty(T, self.topk, dtype=torch.float32, device=dev)
+        self.topi = torch.empty(T, self.topk, dtype=torch.int32, device=dev)
+        cap = capacity(R, self.bm, E)
+        self.sti = torch.empty(cap, dtype=torch.int32, device=dev)
+        self.eids = torch.empty(cap // self.bm, dtype=torch.int32, device=dev)
+        self.ntp = torch.empty(1, dtype=torch.int32, device=dev)
+        self.act = torch.empty(R, I, dtype=BF16, device=dev)
+        self.ybuf = torch.empty(R, H, dtype=BF16, device=dev)
+        self.act_s = torch.empty(T, I, dtype=BF16, device=dev)
+        self.s_out = torch.empty(T, H, dtype=BF16, device=dev)
+        self.out = torch.empty(T, H, dtype=BF16, device=dev)
+        self.ssti, self.seids, self.sntp = shared_layout(T, self.sbm, dev)
+        self.cfg_r = {"BLOCK_M": self.bm, "variant": variant}
+        self.cfg_s = {"BLOCK_M": self.sbm, "variant": variant}
+        self.cfg_topk = {"correction_bias": bias, "scale": scale}
+        self.graph = None
+
+    # ---- the chain -------------------------------------------------------------------
+    def front_end(self, x, r):
+        KN.fused_add_rmsnorm(x, r, self.w_norm, self.h, self.y, {"eps": self.eps})
+        KR.router_gemm(self.y, self.wgt, self.logits, {})
+        KR.topk_only(self.logits, self.topw, self.topi, self.cfg_topk)
+        moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp)
+
+    def experts(self):
+        T, H, I, R = self.T, self.H, self.I, self.T * self.topk
+        moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
+                 R, I, I, True, self.cfg_r)
+        moe_gemm(self.y, 1, self.w13s, self.act_s, None, self.ssti, self.seids, self.sntp,
+                 T, I, I, True, self.cfg_s)
+        moe_gemm(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti, self.eids,
+                 self.ntp, R, H, 0, False, self.cfg_r)
+        moe_gemm(self.act_s, 1, self.w2s, self.s_out, None, self.ssti, self.seids, self.sntp,
+                 T, H, 0, False, self.cfg_s)
+
+    def merge(self):
+        y3 = self.ybuf.view(self.T, self.topk, self.H)
+        _lib.call("glm52_block_merge", _lib.ptr(y3), y3.stride(0), y3.stride(1),
+                  _lib.ptr(self.h), self.h.stride(0), _lib.ptr(self.s_out), self.s_out.stride(0),
+                  _lib.ptr(self.out), self.out.stride(0), self.T, self.H, _lib.stream())
+
+    def forward(self, x: torch.Tensor, r: torch.Tensor) -> torch.Tensor:
+        if x.shape != (self.T, self.H) or r.shape != (self.T, self.H):
+            raise ValueError(f"expected x, r of shape {(self.T, self.H)}")
+        self.front_end(x, r)
+        self.experts()
+        self.merge()
+        return self.out
+
+    __call__ = forward
+
+    # ---- HIP graph -----------------------------------------------------------------
+    def capture(self, x: torch.Tensor, r: torch.Tensor) -> None:
+        """Capture `forward(x, r)` (x and r are read in place on every replay)."""
+        self._gx, self._gr = x, r
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.forward(x, r)  # warm the launch path outside capture
+        torch.cuda.current_stream().wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self.forward(x, r)
+        self.graph = g
+
+    def replay(self) -> torch.Tensor:
+        self.graph.replay()
+        return self.out

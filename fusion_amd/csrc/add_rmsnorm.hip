@@ -1,0 +1,146 @@
+// ResAdd + RMSNorm for the GLM-5.2 MoE block, gfx950.
+//
+// Semantics restate `glm52/reference.py:22-33` (sglang `fused_add_rmsnorm`), and the
+// three launch modes mirror the flag pairs of `glm52/kernels/add_rmsnorm.py:50-190`:
+//
+//   do_add & do_norm : h = bf16(fp32 x + fp32 r); y = bf16(fp32(bf16(h * rstd)) * fp32 w)
+//   do_add only      : h = bf16(fp32 x + fp32 r)
+//   do_norm only     : y from x taken as h
+//
+// The sum of squares runs over the bf16-rounded h, as the reference does.  It is pinned
+// to an order-independent rule so that y (and with it the routing) is bit-reproducible
+// by any implementation: each h^2 is exact in fp32, the squares are summed in fp64
+// (error ~2^-40 relative, far below half an fp32 ulp), and
+//     rstd = fp32(1 / sqrt(ss / N + eps))        evaluated in fp64, rounded once.
+// The reference's fp32 `rsqrt(mean(h^2) + eps)` agrees with it to within an ulp.
+//
+// Mapping: one row of N bf16 is owned by TPR threads (TPR = 64: a wave per row, no
+// barrier; TPR = 256: a workgroup per row, for small T where latency matters).  Each
+// thread owns 8-element chunks c = tid_in_row + j * TPR, reads them with 128-bit loads,
+// keeps h in registers between the reduction and the normalisation, and writes with
+// 128-bit stores, so every byte of x, r, h and y crosses HBM exactly once.
+#include "common.h"
+
+using namespace glm52;
+
+namespace {
+
+template <int TPR, int MAXC, bool DO_ADD, bool DO_NORM>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ h1, uint16_t* __restrict__ out,
+    int64_t sx, int64_t sr, int64_t sh, int64_t so, int T, int N, float eps) {
+  constexpr int ROWS = 256 / TPR;
+  const int tid = threadIdx.x;
+  const int r_in_blk = tid / TPR;
+  const int t_in_row = tid % TPR;
+  const int64_t row = (int64_t)blockIdx.x * ROWS + r_in_blk;
+  const bool row_ok = row < T;
+  const int nchunk = N >> 3;
+
+  float hv[MAXC][8];
+  double ss = 0.0;
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int c = t_in_row + j * TPR;
+    if (row_ok && c < nchunk) {
+      uint4 xv = *reinterpret_cast<const uint4*>(x + row * sx + (int64_t)c * 8);
+      float xf[8];
+      unpack8(xv, xf);
+      if (DO_ADD) {
+        uint4 rv = *reinterpret_cast<const uint4*>(res + row * sr + (int64_t)c * 8);
+        float rf[8];
+        unpack8(rv, rf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xf[q] = xf[q] + rf[q];
+        uint4 hb = pack8(xf);
+        *reinterpret_cast<uint4*>(h1 + row * sh + (int64_t)c * 8) = hb;
+        unpack8(hb, xf);  // the norm consumes the bf16-rounded h
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        hv[j][q] = xf[q];
+        ss += (double)(xf[q] * xf[q]);  // exact square, fp64 sum
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) hv[j][q] = 0.f;
+    }
+  }
+  if (!DO_NORM) return;
+
+  ss = wave_sum_f64(ss);
+  if (TPR > kWave) {
+    __shared__ double part[256 / kWave];
+    const int wid = tid / kWave;
+    if ((tid % kWave) == 0) part[wid] = ss;
+    __syncthreads();
+    constexpr int WPR = TPR / kWave;
+    const int w0 = (wid / WPR) * WPR;
+    double s = 0.0;
+#pragma unroll
+    for (int q = 0; q < WPR; ++q) s += part[w0 + q];
+    ss = s;
+  }
+  if (!row_ok) return;
+  const float rstd = (float)(1.0 / sqrt(ss / (double)N + (double)eps));
+
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int c = t_in_row + j * TPR;
+    if (c < nchunk) {
+      uint4 wv = *reinterpret_cast<const uint4*>(w + (int64_t)c * 8);
+      float wf[8], yf[8];
+      unpack8(wv, wf);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) yf[q] = bf16_to_f32(f32_to_bf16(hv[j][q] * rstd)) * wf[q];
+      *reinterpret_cast<uint4*>(out + row * so + (int64_t)c * 8) = pack8(yf);
+    }
+  }
+}
+
+template <int TPR, int MAXC>
+int launch(const uint16_t* x, const uint16_t* res, const uint16_t* w, uint16_t* h1,
+           uint16_t* out, int64_t sx, int64_t sr, int64_t sh, int64_t so, int T, int N,
+           float eps, bool do_add, bool do_norm, hipStream_t st) {
+  constexpr int ROWS = 256 / TPR;
+  dim3 grid((T + ROWS - 1) / ROWS);
+  if (do_add && do_norm)
+    add_rmsnorm_kernel<TPR, MAXC, true, true><<<grid, 256, 0, st>>>(x, res, w, h1, out, sx, sr, sh, so, T, N, eps);
+  else if (do_add)
+    add_rmsnorm_kernel<TPR, MAXC, true, false><<<grid, 256, 0, st>>>(x, res, w, h1, out, sx, sr, sh, so, T, N, eps);
+  else
+    add_rmsnorm_kernel<TPR, MAXC, false, true><<<grid, 256, 0, st>>>(x, res, w, h1, out, sx, sr, sh, so, T, N, eps);
+  GLM52_RETURN_LAUNCH();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" int glm52_add_rmsnorm(const void* x, const void* res, const void* w, void* h1,
+                                 void* out, int64_t stride_x, int64_t stride_r,
+                                 int64_t stride_h, int64_t stride_o, int T, int N, float eps,
+                                 int do_add, int do_norm, int rows_per_wave_mode,
+                                 hipStream_t stream) {
+  if (T < 0 || N <= 0 || (N % 8) != 0 || N > 8192) return GLM52_EINVAL;
+  if (!do_add && !do_norm) return GLM52_EINVAL;
+  if (T == 0) return GLM52_OK;
+  if (!x || !aligned16(x) || (stride_x % 8)) return GLM52_EINVAL;
+  if (do_add && (!res || !h1 || !aligned16(res) || !aligned16(h1) || (stride_r % 8) || (stride_h % 8)))
+    return GLM52_EINVAL;
+  if (do_norm && (!w || !out || !aligned16(w) || !aligned16(out) || (stride_o % 8)))
+    return GLM52_EINVAL;
+  auto* xx = static_cast<const uint16_t*>(x);
+  auto* rr = static_cast<const uint16_t*>(res);
+  auto* ww = static_cast<const uint16_t*>(w);
+  auto* hh = static_cast<uint16_t*>(h1);
+  auto* oo = static_cast<uint16_t*>(out);
+  // rows_per_wave_mode: 1 -> a wave per row; 0 -> a workgroup per row; -1 -> choose by T.
+  bool wave_per_row = rows_per_wave_mode > 0 || (rows_per_wave_mode < 0 && T >= 512);
+  if (wave_per_row)
+    return launch<64, 16>(xx, rr, ww, hh, oo, stride_x, stride_r, stride_h, stride_o, T, N, eps,
+                          do_add, do_norm, stream);
+  return launch<256, 4>(xx, rr, ww, hh, oo, stride_x, stride_r, stride_h, stride_o, T, N, eps,
+                        do_add, do_norm, stream);
+}

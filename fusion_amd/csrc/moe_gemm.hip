@@ -1,0 +1,447 @@
+// Grouped expert GEMMs of the GLM-5.2 MoE block on bf16 MFMA, gfx950.
+//
+// One source serves both expert GEMMs, like `moe_gateup_kernel`
+// (`glm52/kernels/moe_gateup.py:34-148`) and `moe_down_kernel`
+// (`glm52/kernels/moe_down_merge.py:66-169`), which mirror sglang's `fused_moe_kernel`:
+//
+//   for every padded row slot r of the dispatch layout with token f = sorted_ids[r] < num_valid
+//   and expert e = expert_ids[r / BM]:
+//     gated (w13 + SwiGLU): g = A[f / a_div] . W[e, n, :],  u = A[f / a_div] . W[e, off + n, :]
+//                           C[f, n] = bf16(silu(g) * u)
+//     plain              :  c = A[f / a_div] . W[e, n, :]
+//                           C[f, n] = bf16(c * topk_w[f])   if weighted, else bf16(c)
+//
+// Both operands are K-contiguous (A rows and W rows), which is the native operand layout
+// of `v_mfma_f32_16x16x32_bf16`: a lane supplies 8 consecutive k of one row of A and 8 of
+// one row of W.  Accumulation is fp32.
+//
+// Two mappings, chosen by the host from the number of rows per expert:
+//
+//  * stream (decode): the GEMM is a weight stream.  An item is one 16-row slice of the
+//    layout times 16 output columns; the four waves of a workgroup each take a quarter of
+//    K, load their W fragments straight from HBM into registers (128-bit non-temporal
+//    loads, U steps in flight), and meet in LDS for the split-K sum and the epilogue.
+//
+//  * tiled (prefill): LDS-staged BM x BN tiles with a register-staged double buffer; a
+//    workgroup of four waves computes a BM x BN block with 16x16x32 MFMAs.  Items are
+//    ordered so that the workgroups on one XCD (consecutive ids modulo 8 share an XCD)
+//    walk consecutive row blocks of the same expert, so a W tile is fetched from HBM once
+//    and served from that XCD's L2 to the other row blocks of the expert.
+//
+// Both kernels are persistent: the grid is sized on the host for the worst-case layout
+// and every workgroup loops over the items that exist for the layout the device holds
+// (`num_tokens_post_padded` is read on the device), so no host sync is needed.
+#include "common.h"
+
+using namespace glm52;
+
+namespace {
+
+GLM52_DEV floatx4_t mfma16(const uint4& a, const uint4& b, floatx4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+GLM52_DEV uint4 ldg(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+struct GemmArgs {
+  const uint16_t* A;
+  int64_t sam;
+  int a_div;
+  const uint16_t* W;
+  int64_t swe;
+  int64_t swn;
+  int gu_off;  // row offset of the `up` half inside W[e] (gated only)
+  uint16_t* C;
+  int64_t scm;
+  const float* topw;  // per flat token (weighted only)
+  const int32_t* sti;
+  const int32_t* eids;
+  const int32_t* ntp;
+  int BM;  // block size of the layout
+  int n_out;
+  int K;
+  int num_valid;
+  int group_m;  // tiled mapping: row blocks per swizzle group
+};
+
+// ------------------------------------------------------------------------------------
+// stream mapping
+// ------------------------------------------------------------------------------------
+template <bool GATED, bool WEIGHTED, int U>
+__global__ __launch_bounds__(256) void moe_gemm_stream_kernel(GemmArgs p) {
+  __shared__ float red[4][GATED ? 2 : 1][4][kWave];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  const int r = lane % 16;  // A row / W row within the 16 x 16 tile
+  const int g = lane / 16;  // k group
+
+  const int ntp = *p.ntp;
+  const int num_m = ntp / 16;
+  const int num_n = p.n_out / 16;
+  const int items = num_m * num_n;
+  const int kq = p.K / 4;
+  const int kbeg = wv * kq;
+
+  for (int it = blockIdx.x; it < items; it += gridDim.x) {
+    // n fastest: consecutive workgroups stream different W rows of the same expert
+    const int pid_m = it / num_n;
+    const int pid_n = it % num_n;
+    const int row0 = pid_m * 16;
+    if (p.sti[row0] >= p.num_valid) continue;  // an all-padding slice (BM > 16)
+    const int e = p.eids[row0 / p.BM];
+    const int n0 = pid_n * 16;
+
+    const int tok = p.sti[row0 + r];
+    const bool tok_ok = tok < p.num_valid;
+    const uint16_t* arow = p.A + (int64_t)(tok_ok ? tok / p.a_div : 0) * p.sam + 16 * g;
+    const uint16_t* wg = p.W + (int64_t)e * p.swe + (int64_t)(n0 + r) * p.swn + 16 * g;
+    const uint16_t* wu = wg + (int64_t)p.gu_off * p.swn;
+
+    floatx4_t accg = {0.f, 0.f, 0.f, 0.f};
+    floatx4_t accu = {0.f, 0.f, 0.f, 0.f};
+    int k = kbeg;
+    const int kend = kbeg + kq;
+    for (; k + 64 * U <= kend; k += 64 * U) {
+      uint4 bg[U][2], bu[U][2], av[U][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int kk = k + u * 64;
+        bg[u][0] = ldg_nt(wg + kk);
+        bg[u][1] = ldg_nt(wg + kk + 8);
+        if (GATED) {
+          bu[u][0] = ldg_nt(wu + kk);
+          bu[u][1] = ldg_nt(wu + kk + 8);
+        }
+        if (tok_ok) {
+          av[u][0] = ldg(arow + kk);
+          av[u][1] = ldg(arow + kk + 8);
+        } else {
+          av[u][0] = make_uint4(0, 0, 0, 0);
+          av[u][1] = make_uint4(0, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        accg = mfma16(av[u][0], bg[u][0], accg);
+        accg = mfma16(av[u][1], bg[u][1], accg);
+        if (GATED) {
+          accu = mfma16(av[u][0], bu[u][0], accu);
+          accu = mfma16(av[u][1], bu[u][1], accu);
+        }
+      }
+    }
+    for (; k < kend; k += 64) {
+      const uint4 b0 = ldg_nt(wg + k), b1 = ldg_nt(wg + k + 8);
+      uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
+      if (tok_ok) {
+        a0 = ldg(arow + k);
+        a1 = ldg(arow + k + 8);
+      }
+      accg = mfma16(a0, b0, accg);
+      accg = mfma16(a1, b1, accg);
+      if (GATED) {
+        const uint4 c0 = ldg_nt(wu + k), c1 = ldg_nt(wu + k + 8);
+        accu = mfma16(a0, c0, accu);
+        accu = mfma16(a1, c1, accu);
+      }
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      red[wv][0][i][lane] = accg[i];
+      if (GATED) red[wv][GATED ? 1 : 0][i][lane] = accu[i];
+    }
+    __syncthreads();
+    if (wv == 0) {
+      // lane holds rows 4*g + i of column r of the 16 x 16 output tile
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int orow = 4 * g + i;
+        const int otok = p.sti[row0 + orow];
+        const float sg = ((red[0][0][i][lane] + red[1][0][i][lane]) + red[2][0][i][lane]) + red[3][0][i][lane];
+        float v;
+        if (GATED) {
+          const float su = ((red[0][GATED ? 1 : 0][i][lane] + red[1][GATED ? 1 : 0][i][lane]) +
+                            red[2][GATED ? 1 : 0][i][lane]) + red[3][GATED ? 1 : 0][i][lane];
+          v = silu_mul(sg, su);
+        } else {
+          v = sg;
+        }
+        if (otok < p.num_valid) {
+          if (WEIGHTED) v = v * p.topw[otok];
+          p.C[(int64_t)otok * p.scm + n0 + r] = f32_to_bf16(v);
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// tiled mapping
+// ------------------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool WEIGHTED>
+__global__ __launch_bounds__(256) void moe_gemm_tiled_kernel(GemmArgs p) {
+  static_assert(WM * WN == 4, "four waves");
+  constexpr int NB = GATED ? 2 * BN : BN;  // W rows staged per tile
+  constexpr int LDK = BK + 8;              // +16 B row pad: conflict-free 128-bit reads
+  constexpr int WTM = BM / WM, WTN = BN / WN;
+  constexpr int TM = WTM / 16, TN = WTN / 16;
+  static_assert(TM >= 1 && TN >= 1 && WTM % 16 == 0 && WTN % 16 == 0, "wave tile");
+  constexpr int CPR = BK / 8;  // 16-byte chunks per tile row
+  constexpr int CH_A = BM * CPR, CH_B = NB * CPR;
+  constexpr int QA = (CH_A + 255) / 256, QB = (CH_B + 255) / 256;
+  constexpr int NG = GATED ? 2 : 1;
+
+  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM][LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][NB][LDK];
+  __shared__ int toks[BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  const int wm = wv / WN, wn = wv % WN;
+  const int l16 = lane % 16, lg = lane / 16;
+
+  const int ntp = *p.ntp;
+  const int num_m = ntp / BM;
+  const int num_n = p.n_out / BN;
+  const int items = num_m * num_n;
+  const int nk = p.K / BK;
+
+  // XCD-aware order: ids congruent mod 8 run on one XCD; give each XCD a contiguous
+  // range of logical items.
+  const int per_xcd = (items + 7) / 8;
+  const int span = per_xcd * 8;
+
+  for (int it = blockIdx.x; it < span; it += gridDim.x) {
+    const int L = (it % 8) * per_xcd + it / 8;
+    if (L >= items) continue;
+    // grouped swizzle: GROUP_M row blocks x all column tiles, row block fastest, so a
+    // W tile is reused by the group's row blocks and their A rows stay in L2
+    const int in_group = p.group_m * num_n;
+    const int first_m = (L / in_group) * p.group_m;
+    const int gsz = min(num_m - first_m, p.group_m);
+    const int pid_m = first_m + (L % in_group) % gsz;
+    const int pid_n = (L % in_group) / gsz;
+    const int row0 = pid_m * BM;
+    if (p.sti[row0] >= p.num_valid) continue;  // uniform: an all-padding block
+    const int e = p.eids[pid_m];
+    const int n0 = pid_n * BN;
+
+    for (int q = tid; q < BM; q += 256) toks[q] = p.sti[row0 + q];
+    __syncthreads();
+
+    // per-thread global sources for the A and W chunks it copies
+    const uint16_t* asrc[QA];
+    bool aok[QA];
+    int arow_l[QA], akc[QA];
+#pragma unroll
+    for (int q = 0; q < QA; ++q) {
+      const int c = tid + q * 256;
+      const int rr = c / CPR, kc = c % CPR;
+      arow_l[q] = rr;
+      akc[q] = kc;
+      bool ok = c < CH_A;
+      int t = ok ? toks[rr] : 0;
+      ok = ok && t < p.num_valid;
+      aok[q] = ok;
+      asrc[q] = p.A + (int64_t)(ok ? t / p.a_div : 0) * p.sam + kc * 8;
+    }
+    const uint16_t* bsrc[QB];
+    int brow_l[QB], bkc[QB];
+#pragma unroll
+    for (int q = 0; q < QB; ++q) {
+      const int c = tid + q * 256;
+      const int nn = c / CPR, kc = c % CPR;
+      brow_l[q] = nn;
+      bkc[q] = kc;
+      int grow = n0 + nn;
+      if (GATED && nn >= BN) grow = p.gu_off + n0 + (nn - BN);
+      bsrc[q] = p.W + (int64_t)e * p.swe + (int64_t)(c < CH_B ? grow : n0) * p.swn + kc * 8;
+    }
+
+    uint4 ra[QA], rb[QB];
+    auto gload = [&](int kt) {
+      const int koff = kt * BK;
+#pragma unroll
+      for (int q = 0; q < QA; ++q) ra[q] = aok[q] ? ldg(asrc[q] + koff) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < QB; ++q)
+        if (tid + q * 256 < CH_B) rb[q] = ldg(bsrc[q] + koff);
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+      for (int q = 0; q < QA; ++q)
+        if (tid + q * 256 < CH_A) *reinterpret_cast<uint4*>(&As[buf][arow_l[q]][akc[q] * 8]) = ra[q];
+#pragma unroll
+      for (int q = 0; q < QB; ++q)
+        if (tid + q * 256 < CH_B) *reinterpret_cast<uint4*>(&Bs[buf][brow_l[q]][bkc[q] * 8]) = rb[q];
+    };
+
+    floatx4_t acc[NG][TM][TN];
+#pragma unroll
+    for (int h = 0; h < NG; ++h)
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[h][i][j] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) gload(kt + 1);
+#pragma unroll
+      for (int ks = 0; ks < BK / 32; ++ks) {
+        uint4 af[TM], bf[NG][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const uint4*>(&As[cur][wm * WTM + i * 16 + l16][ks * 32 + lg * 8]);
+#pragma unroll
+        for (int h = 0; h < NG; ++h)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            bf[h][j] = *reinterpret_cast<const uint4*>(&Bs[cur][h * BN + wn * WTN + j * 16 + l16][ks * 32 + lg * 8]);
+#pragma unroll
+        for (int h = 0; h < NG; ++h)
+#pragma unroll
+          for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[h][i][j] = mfma16(af[i], bf[h][j], acc[h][i][j]);
+      }
+      if (kt + 1 < nk) sstore(cur ^ 1);
+      __syncthreads();
+    }
+
+    // epilogue: lane holds rows 4*lg + q of column l16 of each 16 x 16 sub-tile
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int rl = wm * WTM + i * 16 + lg * 4 + q;
+          const int t = toks[rl];
+          if (t < p.num_valid) {
+            float v = GATED ? silu_mul(acc[0][i][j][q], acc[NG - 1][i][j][q]) : acc[0][i][j][q];
+            if (WEIGHTED) v = v * p.topw[t];
+            p.C[(int64_t)t * p.scm + n0 + wn * WTN + j * 16 + l16] = f32_to_bf16(v);
+          }
+        }
+    __syncthreads();
+  }
+}
+
+template <bool GATED, bool WEIGHTED>
+int launch_stream(const GemmArgs& a, int capacity, hipStream_t st) {
+  const int items_max = (capacity / 16) * (a.n_out / 16);
+  int grid = items_max < 4096 ? items_max : 4096;
+  if (grid < 1) grid = 1;
+  moe_gemm_stream_kernel<GATED, WEIGHTED, 4><<<grid, 256, 0, st>>>(a);
+  GLM52_RETURN_LAUNCH();
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool GATED, bool WEIGHTED>
+int launch_tiled(const GemmArgs& a, int capacity, hipStream_t st) {
+  if (a.BM != BM || (a.n_out % BN) || (a.K % BK)) return GLM52_EUNSUPPORTED;
+  const int items_max = (capacity / BM) * (a.n_out / BN);
+  int grid = items_max < 2048 ? items_max : 2048;
+  grid = ((grid + 7) / 8) * 8;
+  moe_gemm_tiled_kernel<BM, BN, BK, WM, WN, GATED, WEIGHTED><<<grid, 256, 0, st>>>(a);
+  GLM52_RETURN_LAUNCH();
+}
+
+template <bool GATED, bool WEIGHTED>
+int launch_tiled_bm(const GemmArgs& a, int capacity, hipStream_t st) {
+  // gated tiles stage 2 * BN W rows; plain tiles stage BN
+  if constexpr (GATED) {
+    switch (a.BM) {
+      case 32: return launch_tiled<32, 64, 64, 1, 4, GATED, WEIGHTED>(a, capacity, st);
+      case 64: return launch_tiled<64, 64, 64, 2, 2, GATED, WEIGHTED>(a, capacity, st);
+      case 128: return launch_tiled<128, 64, 64, 2, 2, GATED, WEIGHTED>(a, capacity, st);
+      default: return GLM52_EUNSUPPORTED;
+    }
+  } else {
+    switch (a.BM) {
+      case 32: return launch_tiled<32, 128, 64, 1, 4, GATED, WEIGHTED>(a, capacity, st);
+      case 64: return launch_tiled<64, 128, 64, 2, 2, GATED, WEIGHTED>(a, capacity, st);
+      case 128: return launch_tiled<128, 128, 64, 2, 2, GATED, WEIGHTED>(a, capacity, st);
+      default: return GLM52_EUNSUPPORTED;
+    }
+  }
+}
+
+bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
+
+}  // namespace
+
+// variant: 0 = choose (stream when BM == 16, tiled otherwise), 1 = stream, 2 = tiled.
+extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
+                              int64_t stride_we, int64_t stride_wn, int gate_up_offset,
+                              void* c, int64_t stride_cm, const float* topk_weights,
+                              const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                              const int32_t* num_tokens_post_padded, int capacity, int block_m,
+                              int num_valid_tokens, int n_out, int k, int gated, int variant,
+                              hipStream_t stream) {
+  if (!a || !w || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
+    return GLM52_EINVAL;
+  if (block_m <= 0 || (block_m % 16) != 0 || capacity < 0 || (capacity % block_m) != 0)
+    return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % 16) != 0 || k <= 0 || (k % 256) != 0 || a_row_div <= 0)
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w) || (stride_am % 8) || (stride_we % 8) || (stride_wn % 8)) return GLM52_EINVAL;
+  if (gated && (gate_up_offset < n_out)) return GLM52_EINVAL;
+  if (capacity == 0) return GLM52_OK;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
+             static_cast<const uint16_t*>(w), stride_we, stride_wn, gate_up_offset,
+             static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4};
+  const bool weighted = topk_weights != nullptr;
+  const bool use_stream = variant == 1 || (variant == 0 && block_m == 16);
+  if (use_stream) {
+    if (gated) return weighted ? launch_stream<true, true>(g, capacity, stream)
+                               : launch_stream<true, false>(g, capacity, stream);
+    return weighted ? launch_stream<false, true>(g, capacity, stream)
+                    : launch_stream<false, false>(g, capacity, stream);
+  }
+  if (gated) return weighted ? launch_tiled_bm<true, true>(g, capacity, stream)
+                             : launch_tiled_bm<true, false>(g, capacity, stream);
+  return weighted ? launch_tiled_bm<false, true>(g, capacity, stream)
+                  : launch_tiled_bm<false, false>(g, capacity, stream);
+}
+
+// Self-test of the MFMA operand/result layout this library assumes: A[r][k] = r + 1 and
+// B[k][c] = (k == c) ? 1 : 0 for k < 16, else 0 -> C[r][c] = r + 1 for c < 16.  Writes
+// the 16 x 16 fp32 result row-major to `out` (256 floats).
+namespace {
+__global__ void mfma_layout_probe(float* out) {
+  const int lane = threadIdx.x;
+  const int r = lane % 16, g = lane / 16;
+  float af[8], bf[8];
+  for (int j = 0; j < 8; ++j) {
+    const int kk = 8 * g + j;
+    af[j] = kk < 16 ? (float)(r + 1) : 0.f;
+    bf[j] = (kk == r) ? 1.f : 0.f;  // B column r has a one at k == r
+  }
+  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+  acc = mfma16(pack8(af), pack8(bf), acc);
+  for (int i = 0; i < 4; ++i) out[(4 * g + i) * 16 + r] = acc[i];
+}
+}  // namespace
+
+extern "C" int glm52_selftest_mfma_layout(float* out, hipStream_t stream) {
+  if (!out) return GLM52_EINVAL;
+  mfma_layout_probe<<<1, 64, 0, stream>>>(out);
+  GLM52_RETURN_LAUNCH();
+}

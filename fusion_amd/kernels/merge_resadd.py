@@ -1,0 +1,51 @@
+"""Fusion #10 -- expert merge + ResAdd, drop-in for `glm52/kernels/merge_resadd.py:243-255`.
+
+    m   = sum_k w[t, k] * fp32 Y[t, k]      (Y unweighted, k in order)
+    out = bf16(fp32(bf16(m)) + fp32 res)    (ROUND_MID=1, the default)
+    out = bf16(m + fp32 res)                (ROUND_MID=0)
+
+`cfg` keys read: `ROUND_MID` (1) and `TOPK` (8).  Mapping keys are accepted and ignored.
+"""
+
+from __future__ import annotations
+
+from .. import _lib
+
+HIDDEN = 6144
+TOPK = 8
+
+
+def _launch(y, wt, res, m, out, cfg, do_merge: bool, do_resadd: bool):
+    _lib.require_gpu(y, wt, res, m, out)
+    topk = int(cfg.get("TOPK", TOPK))
+    if do_merge:
+        T, N = y.shape[0], y.shape[-1]
+        syt, syk = (y.stride(0), y.stride(1)) if y.dim() == 3 else (y.stride(0) * topk, y.stride(0))
+    else:
+        T, N = m.shape
+        syt = syk = 0
+    _lib.call(
+        "glm52_merge_resadd",
+        _lib.ptr(y) if do_merge else None, syt, syk,
+        _lib.ptr(wt) if do_merge else None, wt.stride(0) if (do_merge and wt is not None) else 0,
+        _lib.ptr(res) if do_resadd else None, res.stride(0) if do_resadd else 0,
+        _lib.ptr(m), m.stride(0) if m is not None else 0,
+        _lib.ptr(out) if do_resadd else None, out.stride(0) if do_resadd else 0,
+        T, N, topk, int(do_merge), int(do_resadd), int(bool(cfg.get("ROUND_MID", 1))),
+        _lib.stream(),
+    )
+
+
+def fused_merge_resadd(y, wt, res, out, cfg):
+    """FUSED: read Y [T, topk, H] + RES, write OUT; m is never materialised."""
+    _launch(y, wt, res, None, out, cfg, True, True)
+
+
+def merge_only(y, wt, m, cfg):
+    """unfused kernel #1: m = sum_k w_k * Y[:, k, :]."""
+    _launch(y, wt, None, m, None, cfg, True, False)
+
+
+def resadd_only(m, res, out, cfg):
+    """unfused kernel #2: out = m + res."""
+    _launch(None, None, res, m, out, cfg, False, True)

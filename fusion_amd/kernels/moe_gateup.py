@@ -1,0 +1,93 @@
+"""Fusion #6 -- grouped w13 GEMM (+ SwiGLU), drop-in for `glm52/kernels/moe_gateup.py:199-266`.
+
+`launch_gateup(a, w13, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+num_valid_tokens, top_k, I, cfg, fused)` keeps the reference's arguments and layout
+conventions (`glm52/kernels/REFERENCES.md:41-51`): A rows are gathered with
+`sorted_token_ids // top_k`, `expert_ids[b]` owns BM-block b, padded slots hold
+`num_valid_tokens` and are skipped, and the grid stops at `num_tokens_post_padded`
+(read on the device).  `c` rows are indexed by the flat token id.
+
+  fused=True : c[f, n] = bf16(silu(a . w13[e, n]) * (a . w13[e, I + n]))   ([R, I])
+  fused=False: c[f, n] = bf16(a . w13[e, n])                                ([R, 2I])
+
+`cfg["BLOCK_M"]` must equal the layout's block size (checked).  `cfg["variant"]` may
+force "stream" (weight-streaming decode mapping) or "tiled" (LDS-tiled prefill mapping);
+by default BM = 16 streams and BM in {32, 64, 128} tiles.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2}
+
+
+def check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m: int) -> int:
+    for t, n in ((sorted_token_ids, "sorted_token_ids"), (expert_ids, "expert_ids"),
+                 (num_tokens_post_padded, "num_tokens_post_padded")):
+        if t.dtype != torch.int32 or not t.is_contiguous():
+            raise ValueError(f"{n} must be a contiguous int32 tensor")
+    cap = sorted_token_ids.numel()
+    if block_m <= 0 or cap % block_m or expert_ids.numel() * block_m != cap:
+        raise ValueError(
+            f"cfg BLOCK_M={block_m} does not match the layout "
+            f"({cap} slots, {expert_ids.numel()} blocks)"
+        )
+    return cap
+
+
+def moe_gemm(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, num_valid_tokens, n_out, gate_up_offset, gated, cfg):
+    """Common launcher of the grouped GEMM (both expert GEMMs and the shared expert)."""
+    _lib.require_gpu(a, w, c, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights)
+    if a.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or c.dtype != torch.bfloat16:
+        raise ValueError("grouped GEMM operands are bf16")
+    if a.stride(1) != 1 or w.stride(2) != 1 or c.stride(1) != 1:
+        raise ValueError("A rows, W rows and C rows must be contiguous")
+    if topk_weights is not None and (topk_weights.dtype != torch.float32
+                                     or not topk_weights.is_contiguous()):
+        raise ValueError("topk weights must be a contiguous fp32 tensor")
+    bm = int(cfg["BLOCK_M"])
+    cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    K = a.shape[1]
+    if w.shape[2] != K:
+        raise ValueError(f"K mismatch: A has {K}, W has {w.shape[2]}")
+    variant = VARIANTS[cfg.get("variant")]
+    _lib.call(
+        "glm52_moe_gemm", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w), w.stride(0),
+        w.stride(1), int(gate_up_offset), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights),
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded),
+        cap, bm, int(num_valid_tokens), int(n_out), int(K), int(gated), variant, _lib.stream(),
+    )
+
+
+def smem_bytes(cfg: dict, fused: bool) -> int:
+    """LDS bytes of the tiled mapping for this cfg (the stream mapping uses 8 KB)."""
+    bm = cfg["BLOCK_M"]
+    if bm == 16 or cfg.get("variant") == "stream":
+        return 8192
+    nb = 128
+    return 2 * (bm + nb) * (64 + 8) * 2 + 4 * bm
+
+
+def launch_gateup(a, w13, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                  num_valid_tokens, top_k, I, cfg, fused: bool):
+    """`a`: [T, H] bf16.  `w13`: [E, 2I, H] bf16.  `c`: [T*top_k, I or 2I] bf16."""
+    N = c.shape[1]
+    if fused and N != I:
+        raise ValueError(f"fused output width must be I={I}, got {N}")
+    if not fused and N != 2 * I:
+        raise ValueError(f"unfused output width must be 2I={2 * I}, got {N}")
+    moe_gemm(a, top_k, w13, c, None, sorted_token_ids, expert_ids, num_tokens_post_padded,
+             num_valid_tokens, N, I if fused else 0, fused, cfg)
+
+
+def launch_silu_and_mul(x, y, cfg):
+    _lib.require_gpu(x, y)
+    M, two_i = x.shape
+    if x.stride(1) != 1 or y.stride(1) != 1:
+        raise ValueError("silu_and_mul operands must be row-contiguous")
+    _lib.call("glm52_silu_and_mul", _lib.ptr(x), x.stride(0), _lib.ptr(y), y.stride(0), M,
+              two_i // 2, _lib.stream())

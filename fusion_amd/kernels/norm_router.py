@@ -1,0 +1,104 @@
+"""Router GEMM + sigmoid top-8, drop-in for `glm52/kernels/norm_router.py:251-389`.
+
+Entry points and destination-passing contract are the reference's.  Semantics follow
+`glm52/reference.py:46-79` (not the Triton `topk_only`, which never applied the
+correction bias, `glm52/kernels/norm_router.py:221-238`):
+
+    logits = x2 . Wg          (fp64-accumulated, rounded once to fp32 -- order independent)
+    s      = sigmoid(logits)  (fp64, rounded once to fp32)
+    ids    = top-k of s + correction_bias, descending, lower index first on ties
+    w      = s[ids] / max(sum s[ids], 1e-20) * scale
+
+`cfg` keys read: `scale` (2.5, as `norm_router.py:307`), `NORM_PROB` (True), and the one
+addition this path needs, `correction_bias` (an fp32 [E] device tensor, or None).  The
+fused norm+router variants measured 0.21-0.68x in the reference and are provided as the
+composition of the two kernels they fuse, so callers keep working.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from . import add_rmsnorm as _an
+
+HIDDEN = 6144
+NUM_EXPERTS = 256
+TOP_K = 8
+
+
+def wgt_from_gate(gate_w: torch.Tensor) -> torch.Tensor:
+    """[E, H] (nn.Linear) -> [H, E], the layout the router kernel reads."""
+    return gate_w.t().contiguous()
+
+
+def router_gemm(x2, wgt, logits, cfg):
+    _lib.require_gpu(x2, wgt, logits)
+    if wgt.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError("router weight must be bf16 or fp32")
+    if x2.stride(-1) != 1 or wgt.stride(-1) != 1 or logits.stride(-1) != 1:
+        raise ValueError("router operands must be contiguous along their last dim")
+    T, H = x2.shape
+    E = wgt.shape[1]
+    _lib.call(
+        "glm52_router_logits", _lib.ptr(x2), x2.stride(0), _lib.ptr(wgt), wgt.stride(0),
+        int(wgt.dtype == torch.float32), _lib.ptr(logits), logits.stride(0), T, H, E,
+        _lib.stream(),
+    )
+
+
+def topk_only(logits, topw, topi, cfg):
+    _lib.require_gpu(logits, topw, topi)
+    bias = cfg.get("correction_bias")
+    if bias is not None:
+        _lib.require_gpu(bias)
+        if bias.dtype != torch.float32 or not bias.is_contiguous():
+            raise ValueError("correction_bias must be a contiguous fp32 tensor")
+    T, E = logits.shape
+    k = topi.shape[1]
+    _lib.call(
+        "glm52_router_topk", _lib.ptr(logits), logits.stride(0), _lib.ptr(bias), _lib.ptr(topw),
+        topw.stride(0), _lib.ptr(topi), topi.stride(0), T, E, k, float(cfg.get("scale", 2.5)),
+        int(bool(cfg.get("NORM_PROB", True))), _lib.stream(),
+    )
+
+
+# ---- unfused pieces (norm kernels of fusion #4/#5) -----------------------------------
+def rmsnorm_only(x, w, x2, cfg):
+    _an.norm_only(x, w, x2, cfg)
+
+
+def add_rmsnorm_only(x, res, w, h1, x2, cfg):
+    _an.fused_add_rmsnorm(x, res, w, h1, x2, cfg)
+
+
+# ---- "fused" names, composed from the two kernels ------------------------------------
+def fused_norm_router(x, w, x2, wgt, logits, cfg):
+    _an.norm_only(x, w, x2, cfg)
+    router_gemm(x2, wgt, logits, cfg)
+
+
+def fused_add_norm_router(x, res, w, h1, x2, wgt, logits, cfg):
+    _an.fused_add_rmsnorm(x, res, w, h1, x2, cfg)
+    router_gemm(x2, wgt, logits, cfg)
+
+
+def _logits_scratch(T, wgt, cfg):
+    lg = cfg.get("logits_buf")
+    if lg is None:
+        lg = torch.empty(T, wgt.shape[1], device=wgt.device, dtype=torch.float32)
+    return lg
+
+
+def fused_norm_router_topk(x, w, x2, wgt, topw, topi, cfg):
+    _an.norm_only(x, w, x2, cfg)
+    lg = _logits_scratch(x.shape[0], wgt, cfg)
+    router_gemm(x2, wgt, lg, cfg)
+    topk_only(lg, topw, topi, cfg)
+
+
+def fused_add_norm_router_topk(x, res, w, h1, x2, wgt, topw, topi, cfg):
+    _an.fused_add_rmsnorm(x, res, w, h1, x2, cfg)
+    lg = _logits_scratch(x.shape[0], wgt, cfg)
+    router_gemm(x2, wgt, lg, cfg)
+    topk_only(lg, topw, topi, cfg)

@@ -1,0 +1,107 @@
+/* C-ABI of libglm52_hip.so: the GLM-5.2 MoE FFN block on MI355X (gfx950).
+ *
+ * Every entry point takes raw device pointers, sizes and element strides plus the HIP
+ * stream to launch on; none allocates, none synchronises the host, and all return 0 on
+ * success, a negative GLM52_E* code for an invalid argument, or a positive hipError_t
+ * from the launch.  bf16 tensors are passed as pointers to 16-bit words; base pointers
+ * and row strides of bf16 tensors must be 16-byte aligned (strides multiples of 8).
+ *
+ * Each function replaces one launcher of the reference's Python package
+ * (HansonZhang-cuhksz/fusion, glm52/kernels/*.py), whose Python signatures the package
+ * fusion_amd.kernels keeps; the citation is given per function.
+ */
+#ifndef GLM52_HIP_H
+#define GLM52_HIP_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLM52_OK 0
+#define GLM52_EINVAL (-1)
+#define GLM52_EUNSUPPORTED (-2)
+
+/* ResAdd + RMSNorm.  Replaces add_rmsnorm.fused_add_rmsnorm / add_only / norm_only
+ * (glm52/kernels/add_rmsnorm.py:234-246; kernel :50-190).
+ *   do_add:  h1 = bf16(x + res);  do_norm: out = bf16(bf16(h * rstd) * w), h = h1 or x.
+ *   N % 8 == 0, N <= 8192.  rows_per_wave_mode: 1 wave/row, 0 workgroup/row, -1 by T. */
+int glm52_add_rmsnorm(const void* x, const void* res, const void* w, void* h1, void* out,
+                      int64_t stride_x, int64_t stride_r, int64_t stride_h, int64_t stride_o,
+                      int T, int N, float eps, int do_add, int do_norm, int rows_per_wave_mode,
+                      hipStream_t stream);
+
+/* Router logits [T, E] fp32 = y [T, H] bf16 . wgt [H, E] (bf16, or fp32 if wg_is_f32),
+ * fp64-accumulated and rounded once.  Replaces norm_router.router_gemm
+ * (glm52/kernels/norm_router.py:347-349).  E <= 256, H % 128 == 0. */
+int glm52_router_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wg,
+                        int wg_is_f32, float* logits, int64_t stride_l, int T, int H, int E,
+                        hipStream_t stream);
+
+/* Sigmoid + noaux_tc top-k with optional correction bias (nullable), renormalisation and
+ * scaling.  Replaces norm_router.topk_only (glm52/kernels/norm_router.py:352-354) with
+ * the semantics of glm52/reference.py:46-79.  E <= 256, topk <= 8. */
+int glm52_router_topk(const float* logits, int64_t stride_l, const float* bias, float* topw,
+                      int64_t stride_w, int32_t* topi, int64_t stride_i, int T, int E, int topk,
+                      float scale, int norm_prob, hipStream_t stream);
+
+/* Dispatch layout.  Replaces reference.moe_align_block_size (glm52/reference.py:85-128)
+ * without its host sync: capacity >= numel + E * (block_m - 1), capacity % block_m == 0;
+ * the tail past *num_tokens_post_padded holds the sentinel numel / expert id -1. */
+int glm52_moe_align(const int32_t* topk_ids, int numel, int block_m, int num_experts,
+                    int capacity, int32_t* sorted_token_ids, int32_t* expert_ids,
+                    int32_t* num_tokens_post_padded, hipStream_t stream);
+
+/* Grouped expert GEMM on bf16 MFMA.  Replaces moe_gateup.launch_gateup
+ * (glm52/kernels/moe_gateup.py:199-248; gated = fused SwiGLU, gate_up_offset = I) and
+ * moe_down_merge.launch_down with fuse_merge=False (glm52/kernels/moe_down_merge.py:427-476;
+ * topk_weights non-null = MUL_ROUTED_WEIGHT).  A rows are a[sorted_id / a_row_div],
+ * W is [E, N, K] with K contiguous, C rows are indexed by the flat token id.
+ * variant: 0 auto, 1 weight-streaming, 2 LDS-tiled (block_m in {32, 64, 128}). */
+int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
+                   int64_t stride_we, int64_t stride_wn, int gate_up_offset, void* c,
+                   int64_t stride_cm, const float* topk_weights, const int32_t* sorted_token_ids,
+                   const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                   int capacity, int block_m, int num_valid_tokens, int n_out, int k, int gated,
+                   int variant, hipStream_t stream);
+
+/* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
+ * (glm52/kernels/moe_gateup.py:251-266). */
+int glm52_silu_and_mul(const void* x, int64_t stride_x, void* y, int64_t stride_y, int M, int I,
+                       hipStream_t stream);
+
+/* out[T, N] = bf16(sum_k y[t, k] (+ residual)).  Replaces moe_down_merge.launch_moe_sum
+ * (glm52/kernels/moe_down_merge.py:519-540). */
+int glm52_moe_sum(const void* y, int64_t stride_t, int64_t stride_k, void* out, int64_t stride_o,
+                  const void* residual, int64_t stride_r, int T, int N, int topk, int add_residual,
+                  hipStream_t stream);
+
+/* o = bf16(x + r).  Replaces moe_down_merge.launch_resadd (glm52/kernels/moe_down_merge.py:543-559). */
+int glm52_resadd(const void* x, int64_t stride_x, const void* r, int64_t stride_r, void* o,
+                 int64_t stride_o, int M, int N, hipStream_t stream);
+
+/* Weighted merge + ResAdd.  Replaces merge_resadd.fused_merge_resadd / merge_only /
+ * resadd_only (glm52/kernels/merge_resadd.py:243-255). */
+int glm52_merge_resadd(const void* y, int64_t stride_yt, int64_t stride_yk, const float* wt,
+                       int64_t stride_wt, const void* res, int64_t stride_r, void* m,
+                       int64_t stride_m, void* out, int64_t stride_o, int T, int N, int topk,
+                       int do_merge, int do_resadd, int round_mid, hipStream_t stream);
+
+/* Block tail: out = bf16(sum_{k<8} y[t, k] + h + shared_out) (shared_out nullable).
+ * Replaces the pair launch_moe_sum(add_residual=True) + launch_resadd(shared) of
+ * glm52/bench/bench_layer.py:462-480 with one pass and one rounding. */
+int glm52_block_merge(const void* y, int64_t stride_yt, int64_t stride_yk, const void* h,
+                      int64_t stride_h, const void* shared_out, int64_t stride_s, void* out,
+                      int64_t stride_o, int T, int N, hipStream_t stream);
+
+/* Self-test of the MFMA result layout the GEMMs assume: writes a 16 x 16 fp32 matrix
+ * whose row r is all (r + 1).  No counterpart in the reference. */
+int glm52_selftest_mfma_layout(float* out, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GLM52_HIP_H */

@@ -1,0 +1,89 @@
+"""Write the golden vectors of the reference's own fp32/bf16 path (run once, on the CPU,
+in the build container that holds the reference checkout; the outputs are committed).
+
+    python tests/golden/make_golden.py [/path/to/reference]
+
+It imports `glm52.reference` from the reference checkout only for the functions whose
+bit-level behaviour no closed form pins (torch's reduction order inside `rmsnorm`, the
+router's `F.linear` and `topk`, torch's `silu` rounding, the CPU bf16 `F.linear` inside
+`moe_mlp`, the fp32 product-sum of `expert_merge`).  The dispatch layout is integer work
+pinned by brute force and invariants, so it is not taken from here.
+
+Inputs are not stored: they are regenerated from seeds by `fusion_amd.problem` (and by
+the tiny-shape generator below); the SHA-256 of every input is stored so a drift of the
+generator is caught.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import sys
+from pathlib import Path
+
+import numpy as np
+import torch
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent.parent
+sys.path.insert(0, str(REPO))
+
+from fusion_amd.problem import front_end  # noqa: E402
+
+
+def sha(t: torch.Tensor) -> str:
+    return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def tiny_inputs(seed: int = 99, T: int = 16, H: int = 256, I: int = 128, E: int = 8):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(E, H, generator=g) * H ** -0.5).to(torch.bfloat16)
+    w13 = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    w13s = (torch.randn(1, 2 * I, H, generator=g) * 0.05).to(torch.bfloat16)
+    w2s = (torch.randn(1, H, I, generator=g) * 0.05).to(torch.bfloat16)
+    act_in = torch.randn(T, 2 * I, generator=g).to(torch.bfloat16)
+    y3 = torch.randn(T, 4, H, generator=g).to(torch.bfloat16)
+    wt = torch.rand(T, 4, generator=g).to(torch.float32)
+    return dict(x=x, gate=gate, w13=w13, w2=w2, w13s=w13s, w2s=w2s, act_in=act_in, y3=y3, wt=wt)
+
+
+def main(ref_root: str) -> None:
+    sys.path.insert(0, ref_root)
+    from glm52 import reference as R  # the reference's oracle, CPU only
+
+    # ---- configuration 0: T = 32 front end -------------------------------------------
+    fe = front_end(32)
+    y, h = R.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+    logits, tw, ti = R.router(y, fe.gate, fe.bias)
+    logits0, tw0, ti0 = R.router(y, fe.gate, None)
+    np.savez(
+        HERE / "config0_t32.npz",
+        in_sha=np.array([sha(fe.x), sha(fe.r), sha(fe.w_norm), sha(fe.gate), sha(fe.bias)]),
+        h=u16(h), y=u16(y),
+        logits=logits.numpy(), topk_weights=tw.numpy(), topk_ids=ti.numpy(),
+        logits_nobias=logits0.numpy(), topk_weights_nobias=tw0.numpy(),
+        topk_ids_nobias=ti0.numpy(),
+    )
+
+    # ---- tiny shapes: experts, SwiGLU, merge ------------------------------------------
+    d = tiny_inputs()
+    lg, tws, tis = R.router(d["x"], d["gate"], None, topk=4)
+    routed = R.moe_mlp(d["x"], d["w13"], d["w2"], tws, tis)
+    act = R.silu_and_mul(d["act_in"])
+    merged = R.expert_merge(d["y3"], d["wt"])
+    np.savez(
+        HERE / "tiny_moe.npz",
+        in_sha=np.array([sha(v) for v in d.values()]),
+        topk_weights=tws.numpy(), topk_ids=tis.numpy(), routed=u16(routed),
+        silu=u16(act), merged=u16(merged),
+    )
+    print("wrote", HERE / "config0_t32.npz", HERE / "tiny_moe.npz")
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

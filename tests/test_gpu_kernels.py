@@ -1,0 +1,306 @@
+"""GPU parity of each kernel against the CPU oracle, through the C-ABI library.
+
+Integer and index outputs (ids, dispatch layout) and everything the exact front-end rule
+fixes (h, y, logits, top-k weights) must match bit for bit; the grouped GEMMs are
+checked against fp32 references of the same op within bf16 output rounding.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from fusion_amd import _lib
+from fusion_amd.dispatch import capacity, moe_align_block_size
+from fusion_amd.kernels import add_rmsnorm as KN
+from fusion_amd.kernels import merge_resadd as KM
+from fusion_amd.kernels import moe_down_merge as KD
+from fusion_amd.kernels import moe_gateup as KG
+from fusion_amd.kernels import norm_router as KR
+from fusion_amd.problem import front_end, zipf_bias
+from oracle import glm52_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ------------------------------------------------------------------ MFMA layout
+def test_mfma_layout_selftest(gpu):
+    out = torch.zeros(256, dtype=torch.float32, device=gpu)
+    _lib.call("glm52_selftest_mfma_layout", _lib.ptr(out), _lib.stream())
+    m = out.view(16, 16).cpu()
+    want = torch.arange(1, 17, dtype=torch.float32).unsqueeze(1).expand(16, 16)
+    assert torch.equal(m, want), m
+
+
+# ------------------------------------------------------------------ ResAdd + RMSNorm
+@pytest.mark.parametrize("T", [1, 7, 32, 600])
+@pytest.mark.parametrize("mode", [None, 0, 1])
+def test_add_rmsnorm_bitwise(gpu, T, mode):
+    say(f"add_rmsnorm T={T} mode={mode}")
+    fe = front_end(T)
+    x, r, w = fe.x.to(gpu), fe.r.to(gpu), fe.w_norm.to(gpu)
+    h = torch.empty_like(x)
+    y = torch.empty_like(x)
+    cfg = {} if mode is None else {"WAVE_PER_ROW": mode}
+    KN.fused_add_rmsnorm(x, r, w, h, y, cfg)
+    y_o, h_o = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    assert np.array_equal(u16(h), u16(h_o))
+    assert np.array_equal(u16(y), u16(y_o))
+    # split kernels give the same bits
+    h2, y2 = torch.empty_like(x), torch.empty_like(x)
+    KN.add_only(x, r, h2, cfg)
+    KN.norm_only(h2, w, y2, cfg)
+    assert torch.equal(h2, h) and torch.equal(y2, y)
+
+
+def test_add_rmsnorm_golden_config0(gpu):
+    g = np.load("tests/golden/config0_t32.npz")
+    fe = front_end(32)
+    x, r, w = fe.x.to(gpu), fe.r.to(gpu), fe.w_norm.to(gpu)
+    h, y = torch.empty_like(x), torch.empty_like(x)
+    KN.fused_add_rmsnorm(x, r, w, h, y, {})
+    assert np.array_equal(u16(h), g["h"])
+    assert np.abs(u16(y).astype(np.int32) - g["y"].astype(np.int32)).max() <= 1
+
+
+def test_add_rmsnorm_strided_rows(gpu):
+    fe = front_end(16)
+    big = torch.zeros(16, 6144 + 64, dtype=BF16, device=gpu)
+    big[:, :6144] = fe.x.to(gpu)
+    x = big[:, :6144]
+    r, w = fe.r.to(gpu), fe.w_norm.to(gpu)
+    h, y = torch.empty_like(r), torch.empty_like(r)
+    KN.fused_add_rmsnorm(x, r, w, h, y, {})
+    y_o, h_o = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    assert np.array_equal(u16(y), u16(y_o))
+
+
+# ------------------------------------------------------------------ router
+@pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (32, "normal"),
+                                    (100, "zero"), (2048, "normal"), (2048, "zipf")])
+def test_router_bitwise(gpu, T, bias):
+    say(f"router T={T} bias={bias}")
+    fe = front_end(T, bias=bias)
+    y_o, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    y = y_o.to(gpu)
+    wgt = fe.wgt.to(gpu)
+    logits = torch.empty(T, 256, dtype=torch.float32, device=gpu)
+    KR.router_gemm(y, wgt, logits, {})
+    lg_o = O.router_logits_exact(y_o, fe.wgt)
+    lg = logits.cpu().numpy()
+    assert (lg != lg_o).sum() == 0, f"{(lg != lg_o).sum()} logits differ"
+    topw = torch.empty(T, 8, dtype=torch.float32, device=gpu)
+    topi = torch.empty(T, 8, dtype=torch.int32, device=gpu)
+    b = None if bias == "zero" else fe.bias
+    KR.topk_only(logits, topw, topi, {"correction_bias": None if b is None else b.to(gpu)})
+    w_o, ids_o, _ = O.router_select(lg_o, None if b is None else b.numpy(), 8)
+    assert np.array_equal(topi.cpu().numpy(), ids_o)
+    assert np.array_equal(topw.cpu().numpy(), w_o)
+
+
+def test_router_golden_config0(gpu):
+    g = np.load("tests/golden/config0_t32.npz")
+    fe = front_end(32)
+    x, r, w = fe.x.to(gpu), fe.r.to(gpu), fe.w_norm.to(gpu)
+    h, y = torch.empty_like(x), torch.empty_like(x)
+    KN.fused_add_rmsnorm(x, r, w, h, y, {})
+    topw = torch.empty(32, 8, dtype=torch.float32, device=gpu)
+    topi = torch.empty(32, 8, dtype=torch.int32, device=gpu)
+    KR.fused_norm_router_topk(h, w, y, fe.wgt.to(gpu), topw, topi,
+                              {"correction_bias": fe.bias.to(gpu)})
+    assert np.array_equal(topi.cpu().numpy(), g["topk_ids"])
+    np.testing.assert_allclose(topw.cpu().numpy(), g["topk_weights"], rtol=2e-6, atol=1e-7)
+
+
+# ------------------------------------------------------------------ dispatch layout
+@pytest.mark.parametrize("T,E,k,bm", [(1, 256, 8, 16), (32, 256, 8, 16), (256, 256, 8, 16),
+                                      (2048, 256, 8, 64), (8192, 256, 8, 128), (300, 1, 1, 16),
+                                      (8192, 1, 1, 128), (77, 256, 8, 32)])
+def test_moe_align_bitwise(gpu, T, E, k, bm):
+    say(f"align T={T} E={E} bm={bm}")
+    rng = np.random.default_rng(T + bm)
+    if E == 1:
+        ids = np.zeros((T, 1), dtype=np.int32)
+    else:
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    sti, eids, ntp = moe_align_block_size(torch.from_numpy(ids).to(gpu), bm, E)
+    rs, re_, rn = O.moe_align_block_size(ids, bm, E)
+    n = int(rn[0])
+    assert int(ntp.item()) == n
+    s, e = sti.cpu().numpy(), eids.cpu().numpy()
+    assert np.array_equal(s[:n], rs)
+    assert np.array_equal(e[: n // bm], re_)
+    assert (s[n:] == ids.size).all() and (e[n // bm:] == -1).all()
+    assert s.size == capacity(ids.size, bm, E)
+
+
+def test_moe_align_skewed_routing(gpu):
+    """Configuration 4's Zipf bias concentrates thousands of slots on a few experts."""
+    T = 8192
+    fe = front_end(T, bias="zipf")
+    y_o, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    _, _, ids = O.router_exact(y_o, fe.wgt, zipf_bias().numpy())
+    for bm in (16, 128):
+        sti, eids, ntp = moe_align_block_size(torch.from_numpy(ids).to(gpu), bm, 256)
+        rs, re_, rn = O.moe_align_block_size(ids, bm, 256)
+        n = int(rn[0])
+        assert int(ntp.item()) == n
+        assert np.array_equal(sti.cpu().numpy()[:n], rs)
+        assert np.array_equal(eids.cpu().numpy()[: n // bm], re_)
+
+
+# ------------------------------------------------------------------ grouped GEMMs
+def _gemm_problem(T, E, H, I, k, seed, gpu):
+    g = torch.Generator().manual_seed(seed)
+    a = torch.randn(T, H, generator=g).to(BF16)
+    w13 = (torch.randn(E, 2 * I, H, generator=g) * 0.05).to(BF16)
+    w2 = (torch.randn(E, H, I, generator=g) * 0.05).to(BF16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    tw = torch.rand(T, k, generator=g)
+    return a, w13, w2, ids, tw
+
+
+def _gateup_ref(a, w13, ids, k, I, fused):
+    """fp32 reference of the gated GEMM: rows by flat token f = t * k + j."""
+    T = a.shape[0]
+    out = torch.zeros(T * k, I if fused else 2 * I)
+    af = a.float()
+    flat = ids.reshape(-1)
+    for e in torch.unique(flat).tolist():
+        f = (flat == e).nonzero().view(-1)
+        hh = af[f // k] @ w13[e].float().t()
+        out[f] = (torch.nn.functional.silu(hh[:, :I]) * hh[:, I:]) if fused else hh
+    return out
+
+
+def _down_ref(act, w2, ids, tw):
+    actf = act.float().cpu()
+    flat = ids.reshape(-1)
+    twf = tw.reshape(-1)
+    out = torch.zeros(actf.shape[0], w2.shape[1])
+    for e in torch.unique(flat).tolist():
+        f = (flat == e).nonzero().view(-1)
+        out[f] = twf[f].unsqueeze(1) * (actf[f] @ w2[e].float().t())
+    return out
+
+
+def _close(got: torch.Tensor, ref: torch.Tensor, what: str):
+    got = got.float().cpu()
+    tol = ref.abs() * 2 ** -7 + 1e-2 * ref.abs().max() * 2 ** -7
+    bad = ((got - ref).abs() > tol).sum().item()
+    assert bad == 0, f"{what}: {bad} elements outside bf16 rounding of the fp32 reference"
+
+
+@pytest.mark.parametrize("bm,variant", [(16, "stream"), (32, "tiled"), (64, "tiled"),
+                                        (128, "tiled"), (64, "stream")])
+def test_grouped_gemms_small(gpu, bm, variant):
+    say(f"grouped gemm small bm={bm} {variant}")
+    T, E, H, I, k = 40, 16, 512, 256, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 21 + bm, gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
+    cfg = {"BLOCK_M": bm, "variant": variant}
+    ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
+    act = torch.full((T * k, I), float("nan"), dtype=BF16, device=gpu)
+    KG.launch_gateup(ag, w13g, act, sti, eids, ntp, T * k, k, I, cfg, True)
+    act_ref = _gateup_ref(a, w13, ids, k, I, True)
+    _close(act, act_ref, "w13+SwiGLU")
+    # unfused: [R, 2I] then the split-out SwiGLU
+    inter = torch.empty(T * k, 2 * I, dtype=BF16, device=gpu)
+    KG.launch_gateup(ag, w13g, inter, sti, eids, ntp, T * k, k, I, cfg, False)
+    _close(inter, _gateup_ref(a, w13, ids, k, I, False), "w13 unfused")
+    act2 = torch.empty(T * k, I, dtype=BF16, device=gpu)
+    KG.launch_silu_and_mul(inter, act2, {})
+    d = u16(act2).astype(np.int32) - u16(O.silu_and_mul(inter.cpu())).astype(np.int32)
+    assert np.abs(d).max() <= 1  # device exp vs torch's silu: at most one bf16 ulp
+    # down GEMM, routing weight applied in the epilogue
+    y = torch.full((T * k, H), float("nan"), dtype=BF16, device=gpu)
+    twf = tw.reshape(-1).contiguous()
+    KD.launch_down(act, w2g, y, twf.to(gpu), sti, eids, ntp, T * k, k, cfg, False)
+    _close(y, _down_ref(act, w2, ids, tw), "w2 weighted")
+
+
+def test_grouped_gemm_full_width(gpu):
+    """Real GLM-5.2 widths (H = 6144, I = 2048) on a few experts, both mappings."""
+    T, E, H, I, k = 24, 4, 6144, 2048, 2
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 5, gpu)
+    ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
+    act_ref = _gateup_ref(a, w13, ids, k, I, True)
+    for bm, variant in ((16, "stream"), (32, "tiled")):
+        say(f"grouped gemm full width bm={bm} {variant}")
+        sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
+        cfg = {"BLOCK_M": bm, "variant": variant}
+        act = torch.empty(T * k, I, dtype=BF16, device=gpu)
+        KG.launch_gateup(ag, w13g, act, sti, eids, ntp, T * k, k, I, cfg, True)
+        _close(act, act_ref, f"w13 {variant}")
+        y = torch.empty(T * k, H, dtype=BF16, device=gpu)
+        twf = tw.reshape(-1).contiguous()
+        KD.launch_down(act, w2g, y, twf.to(gpu), sti, eids, ntp, T * k, k, cfg, False)
+        _close(y, _down_ref(act, w2, ids, tw), f"w2 {variant}")
+
+
+def test_layout_mismatch_is_rejected(gpu):
+    T, E, H, I, k = 8, 16, 512, 256, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 1, gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), 16, E)
+    act = torch.empty(T * k, I, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError, match="BLOCK_M"):
+        KG.launch_gateup(a.to(gpu), w13.to(gpu), act, sti, eids, ntp, T * k, k, I,
+                         {"BLOCK_M": 64}, True)
+
+
+# ------------------------------------------------------------------ merges
+def test_merges_bitwise(gpu):
+    g = torch.Generator().manual_seed(4)
+    T, H = 37, 6144
+    y3 = torch.randn(T, 8, H, generator=g).to(BF16)
+    res = torch.randn(T, H, generator=g).to(BF16)
+    s = torch.randn(T, H, generator=g).to(BF16)
+    wt = torch.rand(T, 8, generator=g)
+    y3g, resg, sg, wtg = y3.to(gpu), res.to(gpu), s.to(gpu), wt.to(gpu)
+    out = torch.empty(T, H, dtype=BF16, device=gpu)
+    KD.launch_moe_sum(y3g, out, resg, 8, {}, True)
+    assert torch.equal(out.cpu(), O.moe_sum(y3, res))
+    KD.launch_moe_sum(y3g, out, resg, 8, {}, False)
+    assert torch.equal(out.cpu(), O.moe_sum(y3))
+    KD.launch_resadd(sg, resg, out, {})
+    assert torch.equal(out.cpu(), (s.float() + res.float()).to(BF16))
+    # block tail: bf16((sum_k Y + h) + s)
+    _lib.call("glm52_block_merge", _lib.ptr(y3g), y3g.stride(0), y3g.stride(1), _lib.ptr(resg),
+              resg.stride(0), _lib.ptr(sg), sg.stride(0), _lib.ptr(out), out.stride(0), T, H,
+              _lib.stream())
+    acc = torch.zeros(T, H)
+    for k in range(8):
+        acc = acc + y3[:, k].float()
+    want = ((acc + res.float()) + s.float()).to(BF16)
+    assert torch.equal(out.cpu(), want)
+
+
+@pytest.mark.parametrize("round_mid", [1, 0])
+def test_merge_resadd(gpu, round_mid):
+    g = torch.Generator().manual_seed(5)
+    T, H = 19, 6144
+    y3 = torch.randn(T, 8, H, generator=g).to(BF16)
+    res = torch.randn(T, H, generator=g).to(BF16)
+    wt = torch.rand(T, 8, generator=g)
+    out = torch.empty(T, H, dtype=BF16, device=gpu)
+    KM.fused_merge_resadd(y3.to(gpu), wt.to(gpu), res.to(gpu), out, {"ROUND_MID": round_mid})
+    want = O.merge_resadd(y3, wt, res, round_mid=bool(round_mid))
+    d = (u16(out).astype(np.int32) - u16(want).astype(np.int32))
+    assert np.abs(d).max() <= 1  # fp32 FMA contraction may move one rounding
+    m = torch.empty(T, H, dtype=BF16, device=gpu)
+    KM.merge_only(y3.to(gpu), wt.to(gpu), m, {})
+    out2 = torch.empty(T, H, dtype=BF16, device=gpu)
+    KM.resadd_only(m, res.to(gpu), out2, {})
+    if round_mid:
+        assert torch.equal(out2, out)

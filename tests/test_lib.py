@@ -1,0 +1,85 @@
+"""CPU checks of the C-ABI library and the host-side logic (no GPU calls)."""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from fusion_amd import _lib, block, dispatch
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def declared_symbols() -> list[str]:
+    hdr = (ROOT / "include" / "glm52_hip.h").read_text()
+    return sorted(set(re.findall(r"^int (glm52_\w+)\(", hdr, flags=re.M)))
+
+
+def test_header_declares_every_binding():
+    assert declared_symbols() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    handle = _lib.lib()
+    for name in declared_symbols():
+        assert hasattr(handle, name), name
+
+
+def test_library_binds_torch_hip_runtime():
+    _lib.lib()
+    maps = Path("/proc/self/maps").read_text()
+    hips = {l.split()[-1] for l in maps.splitlines() if "libamdhip64" in l}
+    assert len(hips) == 1, hips
+
+
+def test_argument_errors_are_reported_without_a_gpu():
+    # invalid sizes are rejected on the host before any launch
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.call("glm52_add_rmsnorm", None, None, None, None, None, 0, 0, 0, 0, 4, 7, 1e-5, 1,
+                  1, -1, None)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.call("glm52_moe_align", None, 8, 16, 256, 16, None, None, None, None)
+
+
+def test_launchers_refuse_cpu_tensors():
+    from fusion_amd.kernels import add_rmsnorm as KN
+
+    x = torch.zeros(2, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        KN.fused_add_rmsnorm(x, x, x[0], x, x, {})
+
+
+def test_capacity_bounds_every_layout():
+    from oracle import glm52_oracle as O
+
+    rng = np.random.default_rng(2)
+    for T, bm in ((1, 16), (32, 16), (256, 64), (999, 128)):
+        ids = np.stack([rng.choice(256, 8, replace=False) for _ in range(T)])
+        _, _, ntp = O.moe_align_block_size(ids, bm, 256)
+        cap = dispatch.capacity(T * 8, bm, 256)
+        assert ntp[0] <= cap and cap % bm == 0
+        # worst case: every expert holds count = 1 (mod bm)
+        assert dispatch.capacity(T * 8, bm, 256) >= T * 8 + 256 * (bm - 1)
+
+
+def test_shared_layout_matches_reference_rule():
+    from oracle import glm52_oracle as O
+
+    for T, bm in ((1, 16), (37, 16), (300, 64)):
+        sti, eids, ntp = block.shared_layout(T, bm, "cpu")
+        rs, re_, rn = O.moe_align_block_size(np.zeros((T, 1), dtype=np.int32), bm, 1)
+        n = int(rn[0])
+        assert int(ntp[0]) == n
+        assert np.array_equal(sti[:n].numpy(), rs) and np.array_equal(eids[: n // bm].numpy(), re_)
+        assert (sti[n:] == T).all() and (eids[n // bm:] == -1).all()
+
+
+def test_default_block_m_regimes():
+    assert block.default_block_m(1) == 16
+    assert block.default_block_m(256) == 16
+    assert block.default_block_m(2048) == 64
+    assert block.default_block_m(8192) == 128

@@ -1,0 +1,348 @@
+"""CPU tests that pin the oracle (oracle/glm52_oracle.py) before anything is checked
+against it: golden vectors written by the reference's own `glm52/reference.py`
+(tests/golden/make_golden.py), closed forms, brute force on small inputs and invariants.
+Each check is chosen so that a plausible slip (a dropped bias, a reversed tie rule, a
+missing bf16 round, an off-by-one in the layout) fails it.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import itertools
+from fractions import Fraction
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from fusion_amd.problem import front_end, zipf_bias
+from oracle import glm52_oracle as O
+
+GOLD = Path(__file__).resolve().parent / "golden"
+
+
+def sha(t: torch.Tensor) -> str:
+    return hashlib.sha256(t.contiguous().view(torch.uint8).numpy().tobytes()).hexdigest()
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def bf16_from_u16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(a.astype(np.uint16).view(np.int16)).view(torch.bfloat16)
+
+
+@pytest.fixture(scope="module")
+def cfg0():
+    g = np.load(GOLD / "config0_t32.npz")
+    fe = front_end(32)
+    return g, fe
+
+
+# ---------------------------------------------------------------------- golden vectors
+def test_config0_inputs_regenerate(cfg0):
+    g, fe = cfg0
+    assert list(g["in_sha"]) == [sha(fe.x), sha(fe.r), sha(fe.w_norm), sha(fe.gate), sha(fe.bias)]
+
+
+def test_add_rmsnorm_matches_reference_bitwise(cfg0):
+    g, fe = cfg0
+    y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+    assert np.array_equal(u16(h), g["h"])
+    assert np.array_equal(u16(y), g["y"])
+
+
+def ulp_diff_bf16(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """|a - b| in bf16 ulps for same-sign values (bit patterns as uint16)."""
+    ai, bi = a.astype(np.int32), b.astype(np.int32)
+    return np.abs(ai - bi)
+
+
+def test_add_rmsnorm_exact_within_one_ulp_of_reference(cfg0):
+    g, fe = cfg0
+    y, h = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    assert np.array_equal(u16(h), g["h"])
+    d = ulp_diff_bf16(u16(y), g["y"])
+    assert d.max() <= 1
+    # and it is not a copy of the torch path: the statistic differs in some row
+    ss_torch = fe.x.float().add(fe.r.float()).to(torch.bfloat16).float().pow(2).mean(-1)
+    ss_exact = (h.float().double() ** 2).mean(-1)
+    assert (ss_torch.double() != ss_exact).any()
+
+
+def test_rmsnorm_exact_statistic_closed_form():
+    """rstd from an exact rational sum of squares, rounded once."""
+    g = torch.Generator().manual_seed(12)
+    h = torch.randn(3, 256, generator=g).to(torch.bfloat16)
+    w = torch.ones(256, dtype=torch.bfloat16)
+    y = O.rmsnorm_exact(h, w)
+    for t in range(3):
+        ss = sum(Fraction(float(v)) ** 2 for v in h[t].float().tolist())
+        ms = float(ss) / 256 + float(np.float32(1e-5))
+        rstd = np.float32(1.0 / np.sqrt(ms))
+        want = (torch.from_numpy(h[t].float().numpy() * rstd).to(torch.bfloat16).float()
+                ).to(torch.bfloat16)
+        assert torch.equal(y[t], want)
+
+
+def test_router_exact_on_exact_norm_matches_reference_ids(cfg0):
+    """The full device rule (exact norm, exact logits, exact sigmoid) picks the
+    reference's ids at configuration 0."""
+    g, fe = cfg0
+    y, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    _, w, ids = O.router_exact(y, fe.wgt, fe.bias.numpy())
+    assert np.array_equal(ids, g["topk_ids"])
+    np.testing.assert_allclose(w, g["topk_weights"], rtol=2e-6, atol=1e-7)
+
+
+def test_router_exact_matches_reference_ids(cfg0):
+    g, fe = cfg0
+    y = bf16_from_u16(g["y"]).reshape(32, -1)
+    lg, w, ids = O.router_exact(y, fe.wgt, fe.bias.numpy())
+    assert np.array_equal(ids, g["topk_ids"])
+    np.testing.assert_allclose(w, g["topk_weights"], rtol=2e-6, atol=1e-7)
+    # logits: reference's fp32 F.linear vs the exact rule, against the dynamic range
+    assert np.abs(lg - g["logits"]).max() / np.abs(g["logits"]).max() < 1e-5
+    lg0, w0, ids0 = O.router_exact(y, fe.wgt, None)
+    assert np.array_equal(ids0, g["topk_ids_nobias"])
+    np.testing.assert_allclose(w0, g["topk_weights_nobias"], rtol=2e-6, atol=1e-7)
+
+
+def test_bias_golden_is_discriminative(cfg0):
+    """The biased and unbiased golden ids differ, so dropping the bias fails above."""
+    g, _ = cfg0
+    assert not np.array_equal(g["topk_ids"], g["topk_ids_nobias"])
+
+
+def test_router_reference_restatement_matches_golden(cfg0):
+    g, fe = cfg0
+    y = bf16_from_u16(g["y"]).reshape(32, -1)
+    lg, w, ids = O.router_reference(y, fe.gate, fe.bias)
+    assert np.array_equal(ids.numpy(), g["topk_ids"])
+    assert np.array_equal(lg.numpy(), g["logits"])
+    assert np.array_equal(w.numpy(), g["topk_weights"])
+
+
+def _tiny():
+    import sys
+    sys.path.insert(0, str(GOLD))
+    from make_golden import tiny_inputs  # the same generator that wrote the fixture
+
+    return tiny_inputs()
+
+
+def test_tiny_moe_matches_reference():
+    g = np.load(GOLD / "tiny_moe.npz")
+    d = _tiny()
+    assert list(g["in_sha"]) == [sha(v) for v in d.values()]
+    lg, tw, ti = O.router_reference(d["x"], d["gate"], None, topk=4)
+    assert np.array_equal(ti.numpy(), g["topk_ids"])
+    routed = O.moe_mlp(d["x"], d["w13"], d["w2"], tw, ti)
+    assert np.array_equal(u16(routed), g["routed"])
+    assert np.array_equal(u16(O.silu_and_mul(d["act_in"])), g["silu"])
+    assert np.array_equal(u16(O.expert_merge(d["y3"], d["wt"])), g["merged"])
+
+
+# ---------------------------------------------------------------------- closed forms
+def test_rmsnorm_special_cases():
+    H = 64
+    w = (1.0 + 0.1 * torch.randn(H)).to(torch.bfloat16)
+    z = torch.zeros(3, H, dtype=torch.bfloat16)
+    y, h = O.add_rmsnorm(z, z, w)
+    assert torch.count_nonzero(y.float()) == 0 and torch.count_nonzero(h.float()) == 0
+    for c in (0.5, -3.0, 7.25):
+        x = torch.full((1, H), c, dtype=torch.bfloat16)
+        y = O.rmsnorm(x, w)
+        rn = np.float32(c) / np.sqrt(np.float32(c) * np.float32(c) + np.float32(1e-5))
+        want = (torch.tensor(rn).to(torch.bfloat16).float() * w.float()).to(torch.bfloat16)
+        assert torch.equal(y[0], want)
+
+
+def test_add_is_single_rounding():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(4, 128, generator=g).to(torch.bfloat16)
+    r = torch.randn(4, 128, generator=g).to(torch.bfloat16)
+    _, h = O.add_rmsnorm(x, r, torch.ones(128, dtype=torch.bfloat16))
+    exact = x.double() + r.double()  # exact: two bf16 fit in fp64 without rounding
+    assert torch.equal(h, exact.float().to(torch.bfloat16))
+
+
+def test_silu_and_mul_closed_form():
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(8, 64, generator=g).to(torch.bfloat16)
+    got = O.silu_and_mul(x).float().numpy()
+    gd, ud = x[:, :32].double().numpy(), x[:, 32:].double().numpy()
+    want = gd / (1 + np.exp(-gd)) * ud
+    ulp = np.abs(want) * 2.0 ** -8 + 1e-30
+    assert (np.abs(got - want) <= ulp).all()
+
+
+# ---------------------------------------------------------------------- router
+def _exact_fp32_round(fr: Fraction) -> np.float32:
+    """Correctly rounded Fraction -> fp32 (brute force via the two neighbours)."""
+    f = np.float32(float(fr))
+    cands = [f, np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))]
+    return min(cands, key=lambda c: (abs(Fraction(float(c)) - fr), int(np.float32(c).view(np.int32)) & 1))
+
+
+def test_router_logits_exact_vs_rational_sum():
+    g = torch.Generator().manual_seed(3)
+    T, H, E = 3, 128, 5
+    y = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    wg = (torch.randn(H, E, generator=g) * 0.1).to(torch.bfloat16)
+    got = O.router_logits_exact(y, wg)
+    yf, wf = y.float().numpy(), wg.float().numpy()
+    for t, e in itertools.product(range(T), range(E)):
+        s = sum(Fraction(float(yf[t, k])) * Fraction(float(wf[k, e])) for k in range(H))
+        assert got[t, e] == _exact_fp32_round(s)
+
+
+def _brute_select(logits, bias, k, scale=2.5):
+    s = O.sigmoid_exact(logits)
+    ids, ws = [], []
+    for t in range(s.shape[0]):
+        key = [(-(np.float32(s[t, e] + (0 if bias is None else bias[e]))), e) for e in range(s.shape[1])]
+        sel = [e for _, e in sorted(key)[:k]]
+        sv = [s[t, e] for e in sel]
+        tot = np.float32(0)
+        for v in sv:
+            tot = np.float32(tot + v)
+        ids.append(sel)
+        ws.append([np.float32(np.float32(v / max(tot, np.float32(1e-20))) * np.float32(scale)) for v in sv])
+    return np.array(ws, dtype=np.float32), np.array(ids, dtype=np.int32)
+
+
+def test_router_select_vs_brute_force():
+    rng = np.random.default_rng(5)
+    for E, k in ((16, 8), (256, 8), (9, 3)):
+        lg = rng.normal(size=(20, E)).astype(np.float32)
+        bias = (0.01 * rng.normal(size=E)).astype(np.float32)
+        w, ids, _ = O.router_select(lg, bias, k)
+        bw, bids = _brute_select(lg, bias, k)
+        assert np.array_equal(ids, bids)
+        assert np.array_equal(w, bw)
+
+
+def test_router_ties_lower_index_first():
+    lg = np.zeros((2, 16), dtype=np.float32)  # every score 0.5: a 16-way tie
+    _, ids, _ = O.router_select(lg, None, 8)
+    assert ids.tolist() == [list(range(8))] * 2
+    lg[1, 12] = lg[1, 13] = 1.0  # two tied winners, then the lowest-index ties
+    _, ids, _ = O.router_select(lg, None, 8)
+    assert ids[1].tolist() == [12, 13, 0, 1, 2, 3, 4, 5]
+
+
+def test_router_large_bias_picks_biased_experts_in_bias_order():
+    rng = np.random.default_rng(6)
+    lg = rng.normal(size=(4, 256)).astype(np.float32)
+    bias = np.zeros(256, dtype=np.float32)
+    chosen = [200, 3, 17, 99, 5, 250, 64, 128]
+    for rank, e in enumerate(chosen):
+        bias[e] = 100.0 - rank
+    w, ids, s = O.router_select(lg, bias, 8)
+    assert (ids == np.array(chosen)).all()
+    # weights are the UNBIASED scores renormalised: sum to 2.5, ratios = score ratios
+    np.testing.assert_allclose(w.sum(1), 2.5, rtol=1e-6)
+    np.testing.assert_allclose(w[:, 0] / w[:, 1], s[:, 200] / s[:, 3], rtol=1e-6)
+
+
+def test_router_invariants_zipf():
+    fe = front_end(64, bias="zipf")
+    y, _ = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+    lg, w, ids = O.router_exact(y, fe.wgt, zipf_bias().numpy())
+    assert all(len(set(r)) == 8 for r in ids.tolist())
+    np.testing.assert_allclose(w.sum(1), 2.5, rtol=8 * 2 ** -23)
+    # the skewed bias concentrates load on the low experts
+    counts = np.bincount(ids.reshape(-1), minlength=256)
+    assert counts[:51].sum() > counts[51:].sum() / 4
+
+
+# ---------------------------------------------------------------------- dispatch layout
+def _brute_align(flat, bm, E):
+    """Independent restatement: walk experts, collect indices in order, pad."""
+    sorted_ids, expert_ids = [], []
+    numel = len(flat)
+    for e in range(E):
+        mine = [i for i, v in enumerate(flat) if v == e]
+        if not mine:
+            continue
+        nblk = -(-len(mine) // bm)
+        sorted_ids += mine + [numel] * (nblk * bm - len(mine))
+        expert_ids += [e] * nblk
+    return np.array(sorted_ids, dtype=np.int32), np.array(expert_ids, dtype=np.int32), len(sorted_ids)
+
+
+@pytest.mark.parametrize("T,k,E,bm", [(1, 8, 256, 16), (5, 8, 16, 4), (32, 8, 256, 16),
+                                      (33, 8, 256, 64), (7, 1, 1, 16), (40, 2, 3, 128)])
+def test_align_vs_brute_force(T, k, E, bm):
+    rng = np.random.default_rng(T * 1000 + bm)
+    ids = np.stack([rng.choice(E, size=k, replace=(k > E)) for _ in range(T)]).astype(np.int32)
+    sti, eids, ntp = O.moe_align_block_size(ids, bm, E)
+    bs, be, bn = _brute_align(ids.reshape(-1).tolist(), bm, E)
+    assert ntp[0] == bn
+    assert np.array_equal(sti, bs) and np.array_equal(eids, be)
+
+
+def test_align_invariants_large():
+    rng = np.random.default_rng(11)
+    T, k, E, bm = 2048, 8, 256, 64
+    ids = np.stack([rng.choice(E, size=k, replace=False) for _ in range(T)]).astype(np.int32)
+    sti, eids, ntp = O.moe_align_block_size(ids, bm, E)
+    numel = T * k
+    real = sti[sti < numel]
+    assert np.array_equal(np.sort(real), np.arange(numel))  # a permutation
+    flat = ids.reshape(-1)
+    for b, e in enumerate(eids):
+        blk = sti[b * bm:(b + 1) * bm]
+        blk = blk[blk < numel]
+        assert (flat[blk] == e).all() and (np.diff(blk) > 0).all()
+    counts = np.bincount(flat, minlength=E)
+    assert ntp[0] == (((counts + bm - 1) // bm) * bm).sum()
+    assert set(eids.tolist()) == set(np.nonzero(counts)[0].tolist())
+
+
+# ---------------------------------------------------------------------- experts / merges
+def test_tiny_moe_vs_fp64_textbook():
+    d = _tiny()
+    lg, tw, ti = O.router_reference(d["x"], d["gate"], None, topk=4)
+    got = O.moe_mlp(d["x"], d["w13"], d["w2"], tw, ti).float().numpy()
+    x = d["x"].double().numpy()
+    w13, w2 = d["w13"].double().numpy(), d["w2"].double().numpy()
+    want = np.zeros_like(x)
+    I = w2.shape[2]
+    for t in range(x.shape[0]):
+        for j in range(4):
+            e = int(ti[t, j])
+            hh = w13[e] @ x[t]
+            a = hh[:I] / (1 + np.exp(-hh[:I])) * hh[I:]
+            want[t] += float(tw[t, j]) * (w2[e] @ a)
+    assert np.abs(got - want).max() / np.abs(want).max() < 2e-2
+
+
+def test_shared_expert_vs_fp64():
+    d = _tiny()
+    got = O.shared_expert(d["x"], d["w13s"], d["w2s"]).numpy()
+    x = d["x"].double().numpy()
+    w13, w2 = d["w13s"][0].double().numpy(), d["w2s"][0].double().numpy()
+    hh = x @ w13.T
+    I = w2.shape[1]
+    want = (hh[:, :I] / (1 + np.exp(-hh[:, :I])) * hh[:, I:]) @ w2.T
+    assert np.abs(got - want).max() / np.abs(want).max() < 1e-2
+
+
+def test_merges_closed_form():
+    g = torch.Generator().manual_seed(8)
+    y3 = torch.randn(5, 8, 64, generator=g).to(torch.bfloat16)
+    res = torch.randn(5, 64, generator=g).to(torch.bfloat16)
+    wt = torch.rand(5, 8, generator=g)
+    s = O.moe_sum(y3, res).float().numpy()
+    want = y3.double().sum(1).numpy() + res.double().numpy()
+    assert (np.abs(s - want) <= np.abs(want) * 2 ** -8 + 1e-6).all()
+    m = O.merge_resadd(y3, wt, res, round_mid=False).float().numpy()
+    want = (y3.double() * wt.double().unsqueeze(-1)).sum(1).numpy() + res.double().numpy()
+    assert (np.abs(m - want) <= np.abs(want) * 2 ** -8 + 1e-5).all()
+    # expert_merge is the round_mid merge without the residual
+    assert torch.equal(O.expert_merge(y3, wt),
+                       O.merge_resadd(y3, wt, torch.zeros_like(res), round_mid=True))
