@@ -6,7 +6,8 @@
 //                   (`glm52/kernels/moe_down_merge.py:300-349`)
 //   resadd        : o = bf16(fp32 x + fp32 r)   (`glm52/kernels/moe_down_merge.py:355-381`)
 //   merge_resadd  : m = sum_k w[t, k] * fp32 Y[t, k];  out = bf16(bf16?(m) + fp32 res)
-//                   (`glm52/kernels/merge_resadd.py:59-196`, ROUND_MID optional)
+//                   (`glm52/kernels/merge_resadd.py:59-196`, ROUND_MID optional); each
+//                   product is rounded before its add (no FMA contraction), k in order
 //   block_merge   : out = bf16((sum_k fp32 Y[t, k] + fp32 h) + fp32 s)  -- the tail of the
 //                   block in one pass: routed merge, the residual h and the shared expert
 //                   output s (nullable), one rounding at the end.
@@ -116,6 +117,7 @@ __global__ __launch_bounds__(kBlock) void merge_resadd_kernel(
     const uint16_t* __restrict__ y, int64_t syt, int64_t syk, const float* __restrict__ wt,
     int64_t swt, const uint16_t* __restrict__ res, int64_t sr, uint16_t* __restrict__ m,
     int64_t sm, uint16_t* __restrict__ out, int64_t so, int T, int N, int topk, int round_mid) {
+#pragma clang fp contract(off)
   const int cpr = N / 8;
   const int64_t total = (int64_t)T * cpr;
   for (int64_t q = (int64_t)blockIdx.x * kBlock + threadIdx.x; q < total;
@@ -135,7 +137,7 @@ __global__ __launch_bounds__(kBlock) void merge_resadd_kernel(
           float f[8];
           unpack8(v[k], f);
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[j] += f[j] * w;
+          for (int j = 0; j < 8; ++j) acc[j] = acc[j] + f[j] * w;  // contraction off: no FMA
         }
       }
       if (!DO_RESADD) {
