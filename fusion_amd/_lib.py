@@ -23,7 +23,11 @@ _F = c_float
 # name -> argument types (every entry point returns int: 0 on success)
 SIGNATURES: dict[str, list] = {
     "glm52_add_rmsnorm": [_P, _P, _P, _P, _P, _L, _L, _L, _L, _I, _I, _F, _I, _I, _I, _P],
-    "glm52_router_logits": [_P, _L, _P, _L, _I, _P, _L, _I, _I, _I, _P],
+    "glm52_router_logits": [_P, _L, _P, _L, _L, _I, _P, _L, _P, _L, _I, _I, _I, _P],
+    "glm52_router": [_P, _L, _P, _L, _L, _I, _P, _L, _P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _I,
+                     _F, _I, _P],
+    "glm52_router_topk_align": [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _F, _I, _I, _I, _P, _P,
+                                _P, _P],
     "glm52_router_topk": [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _F, _I, _P],
     "glm52_moe_align": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "glm52_moe_gemm": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I,
@@ -35,6 +39,11 @@ SIGNATURES: dict[str, list] = {
                            _P],
     "glm52_block_merge": [_P, _L, _L, _P, _L, _P, _L, _P, _L, _I, _I, _P],
     "glm52_selftest_mfma_layout": [_P, _P],
+}
+
+# name -> (argument types, return type) for entry points that do not return a status
+QUERIES: dict[str, tuple[list, type]] = {
+    "glm52_router_workspace_bytes": ([_I, _I, _I], c_int64),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported argument combination"}
@@ -55,6 +64,10 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.argtypes = argtypes
             fn.restype = c_int
+        for name, (argtypes, restype) in QUERIES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = restype
         _lib = handle
     return _lib
 
@@ -64,6 +77,10 @@ def call(name: str, *args) -> None:
     if rc != 0:
         why = ERRORS.get(rc, f"hipError {rc}")
         raise RuntimeError(f"{name} failed: {why}")
+
+
+def query(name: str, *args):
+    return getattr(lib(), name)(*args)
 
 
 def stream() -> int:

@@ -4,9 +4,10 @@ Chain (`glm52/bench/bench_layer.py:395-481`, configuration `H_f3_f10` without o_
 the routing computed live instead of frozen, and the tail fused):
 
     1. ResAdd+RMSNorm           h = bf16(x + r), y = RMSNorm(h)           add_rmsnorm
-    2. router logits            fp64-accumulated, fp32 out                router_gemm
-    3. sigmoid + biased top-8   ids, weights                              topk_only
+    2. router logits            fp64-exact; decode: a wave per gate row   router (launch 1)
+    3. sigmoid + biased top-8   ids, weights                              router (launch 2)
     4. dispatch/align           sglang layout, count kept on the device  moe_align
+                                (decode: 3 and 4 are one launch, router_topk_align)
     5. routed w13 + SwiGLU      act[8T, I]                                moe_gemm (gated)
     6. shared w13 + SwiGLU      act_s[T, I]                               moe_gemm (gated, E=1)
     7. routed w2 (weighted)     Y[8T, H] = w * (act . w2^T)               moe_gemm
@@ -25,7 +26,7 @@ import torch
 
 from . import config as C
 from . import _lib
-from .dispatch import capacity, moe_align_block_size_into
+from .dispatch import capacity, moe_align_block_size_into, topk_align_into
 from .kernels import add_rmsnorm as KN
 from .kernels import norm_router as KR
 from .kernels.moe_gateup import moe_gemm
@@ -95,15 +96,26 @@ class MoEBlock:
         self.ssti, self.seids, self.sntp = shared_layout(T, self.sbm, dev)
         self.cfg_r = {"BLOCK_M": self.bm, "variant": variant}
         self.cfg_s = {"BLOCK_M": self.sbm, "variant": variant}
-        self.cfg_topk = {"correction_bias": bias, "scale": scale}
+        # decode: the [E, H] gate rows feed the one-row-per-wave router, and top-k plus
+        # the dispatch layout run as one single-workgroup launch
+        self.decode = T <= 16 and T * self.topk <= 256
+        self.wgt_rows = wgt.t().contiguous().t() if self.decode else None
+        need = KR.workspace_bytes(T, H, E)
+        self.router_ws = torch.empty(max(need, 8), dtype=torch.uint8, device=dev)
+        self.cfg_topk = {"correction_bias": bias, "scale": scale, "workspace": self.router_ws}
         self.graph = None
 
     # ---- the chain -------------------------------------------------------------------
     def front_end(self, x, r):
         KN.fused_add_rmsnorm(x, r, self.w_norm, self.h, self.y, {"eps": self.eps})
-        KR.router_gemm(self.y, self.wgt, self.logits, {})
-        KR.topk_only(self.logits, self.topw, self.topi, self.cfg_topk)
-        moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp)
+        if self.decode:
+            # gate rows streamed once by 64 workgroups; top-k and layout in one launch
+            KR.router_gemm(self.y, self.wgt_rows, self.logits, self.cfg_topk)
+            topk_align_into(self.logits, self.topw, self.topi, self.cfg_topk, self.bm, self.E,
+                            self.sti, self.eids, self.ntp)
+        else:
+            KR.router(self.y, self.wgt, self.logits, self.topw, self.topi, self.cfg_topk)
+            moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp)
 
     def experts(self):
         T, H, I, R = self.T, self.H, self.I, self.T * self.topk

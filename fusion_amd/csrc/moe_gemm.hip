@@ -421,9 +421,13 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
                   : launch_tiled_bm<false, false>(g, capacity, stream);
 }
 
-// Self-test of the MFMA operand/result layout this library assumes: A[r][k] = r + 1 and
-// B[k][c] = (k == c) ? 1 : 0 for k < 16, else 0 -> C[r][c] = r + 1 for c < 16.  Writes
-// the 16 x 16 fp32 result row-major to `out` (256 floats).
+// Self-test of the MFMA result layouts this library assumes, for the bf16 16x16x32 and
+// the fp64 16x16x4 instructions: A[r][k] = r + 1 for the first 16 k, B = identity on
+// those k -> C[r][c] = r + 1.  Lane l supplies row / column l % 16 and k group l / 16;
+// the result's register i of lane l is row 4 (l / 16) + i for bf16 and (l / 16) + 4 i
+// for fp64, column l % 16 in both.  Writes two 16 x 16 fp32 matrices row-major to `out`
+// (512 floats): [0, 256) from the bf16 MFMA, [256, 512) from the fp64 MFMA.
+typedef double doublex4_t __attribute__((ext_vector_type(4)));
 namespace {
 __global__ void mfma_layout_probe(float* out) {
   const int lane = threadIdx.x;
@@ -437,6 +441,15 @@ __global__ void mfma_layout_probe(float* out) {
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
   acc = mfma16(pack8(af), pack8(bf), acc);
   for (int i = 0; i < 4; ++i) out[(4 * g + i) * 16 + r] = acc[i];
+  // fp64: four k-steps of 4 cover k = 0..15; lane supplies A[r][k0 + g], B[k0 + g][r]
+  doublex4_t d = {0.0, 0.0, 0.0, 0.0};
+  for (int k0 = 0; k0 < 16; k0 += 4) {
+    const double a = (double)(r + 1);
+    const double b = (k0 + g == r) ? 1.0 : 0.0;
+    d = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, d, 0, 0, 0);
+  }
+  // fp64 result layout: register i of lane (r, g) is row g + 4 i
+  for (int i = 0; i < 4; ++i) out[256 + (g + 4 * i) * 16 + r] = (float)d[i];
 }
 }  // namespace
 

@@ -1,4 +1,4 @@
-// GLM-5.2 router: fp32 logits, sigmoid scores, noaux_tc bias-corrected top-8, gfx950.
+// GLM-5.2 router: fp32 logits, sigmoid scores, noaux_tc bias-corrected top-k, gfx950.
 //
 // Semantics restate `glm52/reference.py:46-79` (n_group = topk_group = 1, so there is no
 // group mask):
@@ -6,202 +6,321 @@
 //   logits = y . Wg^T                          (fp32 result)
 //   s      = sigmoid(logits)                   (fp32)
 //   choice = s + bias                          (fp32 add; bias may be absent)
-//   ids    = the 8 largest choices, in descending order, lower index first on ties
+//   ids    = the k largest choices, in descending order, lower index first on ties
 //   w      = s[ids] / max(sum_k s[ids], 1e-20) * scale      (or s[ids] * scale)
 //
 // Bit-exact routing.  A 6144-term fp32 dot product depends on summation order, so two
 // implementations that sum differently can disagree on an id whenever the 8th and 9th
-// choices are within an ulp or two.  This kernel therefore pins the arithmetic to a rule
-// that does not depend on order: every bf16 x bf16 product is exact in fp64, the sum is
-// carried in fp64 (its rounding error, ~2^-53 relative, is far below half an fp32 ulp),
-// and the result is rounded once to fp32.  The sigmoid is evaluated in fp64 and rounded
-// once to fp32 as well.  The CPU oracle applies the same rule, so ids agree bit for bit.
+// choices are within an ulp or two.  The arithmetic is therefore pinned to a rule that
+// does not depend on order: every bf16 x bf16 product is exact in fp64, the sum is
+// carried in fp64 (its rounding error is far below half an fp32 ulp), and the result is
+// rounded once to fp32.  The sigmoid is evaluated in fp64 and rounded once to fp32.  The
+// CPU oracle applies the same rule, so ids agree bit for bit.
 //
-// The reference kernel's layout for the gate weight is [H, E] (`wgt_from_gate`,
-// `glm52/kernels/norm_router.py:251-255`); it is what `router_gemm` consumes here too.
-#include "common.h"
+// Two mappings, picked by the gate's layout.  Rows ([E, H], K contiguous, used at small
+// T): a wave per expert streams its row once (`router_rows_kernel`).  Columns ([H, E],
+// the reference kernel's layout): the logits run on the fp64 matrix cores
+// (`v_mfma_f64_16x16x4_f64`): a workgroup owns 16
+// tokens x all experts, each of its four waves 64 experts (four 16 x 16 fp64 tiles), and
+// walks a K slice staging y (as fp64) and the gate weight (as stored) in LDS.  Small T
+// splits K over KS workgroups; their fp64 partials land in a caller-provided workspace
+// and are summed in a fixed order (by `router_reduce_kernel`, or inside the top-k kernel)
+// before the single rounding to fp32.
+//
+// Top-k: one wave per token.  Each expert's rank is the number of experts that beat it
+// under the (choice descending, index ascending) order; ranks form a permutation, and
+// the experts of rank < k land in slot = rank, already sorted.  No sequential rounds.
+//
+// The gate weight layout is the reference kernel's [H, E] (`wgt_from_gate`,
+// `glm52/kernels/norm_router.py:251-255`).
+#include "select.h"
 
 using namespace glm52;
 
+typedef double doublex4_t __attribute__((ext_vector_type(4)));
+
 namespace {
 
-constexpr int KC = 32;  // k-chunk staged in LDS per wave
+constexpr int KC = 32;    // k rows staged per chunk
+constexpr int TB = 16;    // tokens per workgroup (one fp64 MFMA tile)
+constexpr int EMAX = kMaxE;
 
-// grid = (ceil(T / BT), ceil(E / 64)); block = 256 (4 waves, each a quarter of K).
-template <int BT, bool WG_F32>
+GLM52_DEV doublex4_t mfma64(double a, double b, doublex4_t c) {
+  return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// grid = (ceil(T / 16), KS); block = 256.  KS == 1: fp32 logits out; else fp64 partials.
+template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swg,
-    float* __restrict__ logits, int64_t sl, int T, int H, int E) {
-  constexpr int NACC = BT >= 4 ? 1 : 4 / BT;  // independent chains for small BT
-  __shared__ double ys[4][BT][KC];
-  __shared__ double red[4][BT][kWave];
+    float* __restrict__ logits, int64_t sl, double* __restrict__ part, int T, int H, int E) {
+  using WT = typename std::conditional<WG_F32, float, uint16_t>::type;
+  __shared__ double ys[TB][KC + 1];
+  __shared__ WT ws[KC][EMAX + (WG_F32 ? 4 : 8)];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wv = tid / kWave;
-  const int t0 = blockIdx.x * BT;
-  const int e = blockIdx.y * kWave + lane;
-  const bool e_ok = e < E;
-  const int kq = H / 4;
-  const int kbeg = wv * kq;
+  const int t0 = blockIdx.x * TB;
+  const int KS = gridDim.y;
+  const int ksl = H / KS;
+  const int kbeg = blockIdx.y * ksl;
+  const WT* wg = static_cast<const WT*>(wg_raw);
+  const int ntile = E / 16;
 
-  double acc[BT][NACC];
+  doublex4_t acc[4];
 #pragma unroll
-  for (int t = 0; t < BT; ++t)
-#pragma unroll
-    for (int q = 0; q < NACC; ++q) acc[t][q] = 0.0;
+  for (int j = 0; j < 4; ++j) acc[j] = doublex4_t{0.0, 0.0, 0.0, 0.0};
 
-  for (int k0 = kbeg; k0 < kbeg + kq; k0 += KC) {
-    // stage y[t0 .. t0+BT)[k0 .. k0+KC) as fp64 in this wave's LDS slice
-    for (int idx = lane; idx < BT * KC; idx += kWave) {
-      const int t = idx / KC, kk = idx % KC;
-      double v = 0.0;
-      if (t0 + t < T) v = (double)bf16_to_f32(y[(int64_t)(t0 + t) * sy + k0 + kk]);
-      ys[wv][t][kk] = v;
+  for (int k0 = kbeg; k0 < kbeg + ksl; k0 += KC) {
+    // stage y[t0 .. t0+16)[k0 .. k0+32) as fp64 and Wg[k0 .. k0+32)[0 .. E)
+    for (int q = tid; q < TB * KC; q += 256) {
+      const int t = q / KC, kk = q % KC;
+      ys[t][kk] = (t0 + t < T) ? (double)bf16_to_f32(y[(int64_t)(t0 + t) * sy + k0 + kk]) : 0.0;
+    }
+    constexpr int VEC = WG_F32 ? 4 : 8;  // 16-byte vectors of the gate row
+    const int vpr = E / VEC;
+    for (int q = tid; q < KC * vpr; q += 256) {
+      const int kk = q / vpr, c = q % vpr;
+      *reinterpret_cast<uint4*>(&ws[kk][c * VEC]) =
+          *reinterpret_cast<const uint4*>(wg + (int64_t)(k0 + kk) * swg + c * VEC);
     }
     __syncthreads();
-#pragma unroll 4
-    for (int kk = 0; kk < KC; ++kk) {
-      double wvv = 0.0;
-      if (e_ok) {
-        const int64_t off = (int64_t)(k0 + kk) * swg + e;
-        wvv = WG_F32 ? (double)static_cast<const float*>(wg_raw)[off]
-                     : (double)bf16_to_f32(static_cast<const uint16_t*>(wg_raw)[off]);
-      }
 #pragma unroll
-      for (int t = 0; t < BT; ++t) acc[t][kk % NACC] = fma(ys[wv][t][kk], wvv, acc[t][kk % NACC]);
+    for (int k4 = 0; k4 < KC; k4 += 4) {
+      const double a = ys[lane % 16][k4 + lane / 16];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int tile = wv * 4 + j;
+        if (tile < ntile) {
+          const WT raw = ws[k4 + lane / 16][tile * 16 + lane % 16];
+          double b;
+          if constexpr (WG_F32) b = (double)raw;
+          else b = (double)bf16_to_f32(raw);
+          acc[j] = mfma64(a, b, acc[j]);
+        }
+      }
     }
     __syncthreads();
   }
 
+  // the fp64 MFMA result layout: register v of lane l holds row (l / 16) + 4 v (token)
+  // and column l % 16 (expert) of the tile -- unlike the bf16 16x16x32 layout, where the
+  // row is 4 (l / 16) + v
 #pragma unroll
-  for (int t = 0; t < BT; ++t) {
-    double s = 0.0;
+  for (int j = 0; j < 4; ++j) {
+    const int tile = wv * 4 + j;
+    if (tile >= ntile) continue;
+    const int e = tile * 16 + lane % 16;
 #pragma unroll
-    for (int q = 0; q < NACC; ++q) s += acc[t][q];
-    red[wv][t][lane] = s;
+    for (int v = 0; v < 4; ++v) {
+      const int t = t0 + lane / 16 + 4 * v;
+      if (t >= T) continue;
+      if (KS == 1) logits[(int64_t)t * sl + e] = (float)acc[j][v];
+      else part[((int64_t)blockIdx.y * T + t) * E + e] = acc[j][v];
+    }
+  }
+}
+
+// Row layout (gate as [E, H], rows contiguous), for small T: a wave per expert streams
+// its 12 KB gate row once, each lane 8 consecutive k per step with 16-byte loads, and
+// dots it with the T <= RT token rows staged in LDS; the fp64 lane sums meet in a fixed
+// butterfly.  grid = (ceil(E / 4), ceil(T / RT)); block = 256.
+constexpr int RT = 4;
+constexpr int HMAX = 8192;
+
+template <bool WG_F32>
+__global__ __launch_bounds__(256) void router_rows_kernel(
+    const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swe,
+    float* __restrict__ logits, int64_t sl, int T, int H, int E) {
+  extern __shared__ __attribute__((aligned(16))) uint16_t ys[];  // [min(RT, T - t0)][H]
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int e = blockIdx.x * 4 + tid / kWave;
+  const int t0 = blockIdx.y * RT;
+  const int nt = min(RT, T - t0);
+  const int nch = H / 8;
+  for (int q = tid; q < nt * nch; q += 256) {
+    const int t = q / nch, c = q % nch;
+    *reinterpret_cast<uint4*>(&ys[t * H + c * 8]) =
+        *reinterpret_cast<const uint4*>(y + (int64_t)(t0 + t) * sy + c * 8);
   }
   __syncthreads();
-  for (int t = wv; t < BT; t += 4) {
-    if (t0 + t < T && e_ok) {
-      const double s = ((red[0][t][lane] + red[1][t][lane]) + red[2][t][lane]) + red[3][t][lane];
-      logits[(int64_t)(t0 + t) * sl + e] = (float)s;
+  if (e >= E) return;
+  double acc[RT];
+#pragma unroll
+  for (int t = 0; t < RT; ++t) acc[t] = 0.0;
+  for (int c = lane; c < nch; c += kWave) {
+    float wf[8];
+    if constexpr (WG_F32) {
+      const float* wr = static_cast<const float*>(wg_raw) + (int64_t)e * swe + c * 8;
+      const float4 a = *reinterpret_cast<const float4*>(wr);
+      const float4 b = *reinterpret_cast<const float4*>(wr + 4);
+      wf[0] = a.x; wf[1] = a.y; wf[2] = a.z; wf[3] = a.w;
+      wf[4] = b.x; wf[5] = b.y; wf[6] = b.z; wf[7] = b.w;
+    } else {
+      unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(wg_raw) +
+                                              (int64_t)e * swe + c * 8), wf);
     }
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      if (t < nt) {
+        float yf[8];
+        unpack8(*reinterpret_cast<const uint4*>(&ys[t * H + c * 8]), yf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[t] = fma((double)yf[q], (double)wf[q], acc[t]);
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    const double s = wave_sum_f64(acc[t]);
+    if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * sl + e] = (float)s;
   }
 }
 
-// One wave per token; E <= 256 experts, four per lane.
-struct Cand {
-  float v;  // selection key (score + bias)
-  int i;    // expert index
-  float s;  // unbiased score
-};
-
-GLM52_DEV bool better(const Cand& a, const Cand& b) {
-  return a.v > b.v || (a.v == b.v && a.i < b.i);
+// logits[t, e] = fp32(sum_ks part[ks, t, e]), ks in order.
+__global__ __launch_bounds__(256) void router_reduce_kernel(const double* __restrict__ part,
+                                                            float* __restrict__ logits,
+                                                            int64_t sl, int T, int E, int KS) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= (int64_t)T * E) return;
+  const int64_t t = q / E;
+  const int e = (int)(q % E);
+  double s = 0.0;
+  for (int ks0 = 0; ks0 < KS; ks0 += 8) {  // 8 loads in flight, adds in ks order
+    double v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = ks0 + i < KS ? part[(int64_t)(ks0 + i) * T * E + q] : 0.0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      if (ks0 + i < KS) s += v[i];
+  }
+  logits[t * sl + e] = (float)s;
 }
 
+// One wave per token, four tokens per workgroup.  If `part` is non-null the fp64
+// partials are reduced here in ks order (and the logits written); else logits are read.
 __global__ __launch_bounds__(256) void router_topk_kernel(
-    const float* __restrict__ logits, int64_t sl, const float* __restrict__ bias,
-    float* __restrict__ topw, int64_t stw, int32_t* __restrict__ topi, int64_t sti, int T,
-    int E, int topk, float scale, int norm_prob) {
+    float* __restrict__ logits, int64_t sl, const double* __restrict__ part, int KS,
+    const float* __restrict__ bias, float* __restrict__ topw, int64_t stw,
+    int32_t* __restrict__ topi, int64_t sti, int T, int E, int topk, float scale,
+    int norm_prob) {
+  __shared__ float keys[4][kMaxE];
+  __shared__ float sel_s[4][8];
+  __shared__ int sel_i[4][8];
   const int lane = threadIdx.x % kWave;
-  const int64_t t = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
-  if (t >= T) return;
+  const int wv = threadIdx.x / kWave;
+  const int64_t t = (int64_t)blockIdx.x * 4 + wv;
+  const bool t_ok = t < T;
 
-  float key[4], sc[4];
-  bool taken[4];
+  float lg[4], sc[4], key[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + j * kWave;
-    taken[j] = !(e < E);
-    key[j] = -INFINITY;
-    sc[j] = 0.f;
-    if (e < E) {
-      const double lg = (double)logits[t * sl + e];
-      const float s = (float)(1.0 / (1.0 + exp(-lg)));
-      sc[j] = s;
-      key[j] = bias ? s + bias[e] : s;
-    }
-  }
-
-  float sel_s[8];
-  int sel_i[8];
+    lg[j] = 0.f;
+    if (t_ok && e < E) {
+      if (part) {
+        double s = 0.0;
+        for (int ks0 = 0; ks0 < KS; ks0 += 8) {  // 8 loads in flight, adds in ks order
+          double v[8];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    sel_s[k] = 0.f;
-    sel_i[k] = 0;
-    if (k >= topk) continue;
-    Cand best{-INFINITY, 0x7fffffff, 0.f};
+          for (int i = 0; i < 8; ++i)
+            v[i] = ks0 + i < KS ? part[((int64_t)(ks0 + i) * T + t) * E + e] : 0.0;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      Cand c{key[j], lane + j * kWave, sc[j]};
-      if (!taken[j] && (best.i == 0x7fffffff || better(c, best))) best = c;
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-      Cand o;
-      o.v = __shfl_xor(best.v, off, kWave);
-      o.i = __shfl_xor(best.i, off, kWave);
-      o.s = __shfl_xor(best.s, off, kWave);
-      if (o.i != 0x7fffffff && (best.i == 0x7fffffff || better(o, best))) best = o;
-    }
-    sel_s[k] = best.s;
-    sel_i[k] = best.i;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (lane + j * kWave == best.i) taken[j] = true;
-  }
-
-  float sum = 0.f;
-#pragma unroll
-  for (int k = 0; k < 8; ++k)
-    if (k < topk) sum += sel_s[k];
-  const float denom = fmaxf(sum, 1e-20f);
-  if (lane < topk) {
-    float s = 0.f;
-    int id = 0;
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      if (k == lane) {
-        s = sel_s[k];
-        id = sel_i[k];
+          for (int i = 0; i < 8; ++i)
+            if (ks0 + i < KS) s += v[i];
+        }
+        lg[j] = (float)s;
+        logits[t * sl + e] = lg[j];
+      } else {
+        lg[j] = logits[t * sl + e];
       }
-    const float wgt = norm_prob ? (s / denom) * scale : s * scale;
-    topw[t * stw + lane] = wgt;
+    }
+  }
+  topk_keys(lg, bias, E, t_ok, sc, key, keys[wv]);
+  __syncthreads();
+  if (t_ok) topk_rank(keys[wv], sc, key, E, topk, sel_s[wv], sel_i[wv]);
+  __syncthreads();
+  if (t_ok && lane < topk) {
+    float w;
+    int id;
+    topk_weight(sel_s[wv], sel_i[wv], topk, scale, norm_prob, &w, &id);
+    topw[t * stw + lane] = w;
     topi[t * sti + lane] = id;
   }
 }
 
+// K split for T tokens: enough workgroups to cover the chip at small T.
+int choose_ks(int T, int H) {
+  const int tblocks = (T + TB - 1) / TB;
+  int ks = 1;
+  while (tblocks * ks < 128 && ks < 16 && (H % (KC * ks * 2)) == 0) ks *= 2;
+  return ks;
+}
+
+}  // namespace
+
+extern "C" int64_t glm52_router_workspace_bytes(int T, int H, int E) {
+  const int ks = choose_ks(T, H);
+  return ks == 1 ? 0 : (int64_t)ks * T * E * (int64_t)sizeof(double);
+}
+
+namespace {
+int launch_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                  int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                  void* workspace, int64_t workspace_bytes, int T, int H, int E, int* ks_out,
+                  hipStream_t stream) {
+  if (T < 0 || H <= 0 || E <= 0 || E > EMAX || (E % 16) != 0 || (H % KC) != 0) return GLM52_EINVAL;
+  if (!y || !wgt || !logits || stride_l < E || stride_y < H || (stride_y % 8) ||
+      (reinterpret_cast<uintptr_t>(y) & 15u))
+    return GLM52_EINVAL;
+  // the gate is read with 16-byte vectors along its contiguous dim
+  if (reinterpret_cast<uintptr_t>(wgt) & 15u) return GLM52_EINVAL;
+  const int vec = wg_is_f32 ? 4 : 8;
+  if (stride_wk == 1) {  // rows layout [E, H]
+    if (stride_we < H || (stride_we % vec) || H > HMAX) return GLM52_EINVAL;
+    *ks_out = 1;
+    if (T == 0) return GLM52_OK;
+    dim3 grid((E + 3) / 4, (T + RT - 1) / RT);
+    const size_t lds = (size_t)(T < RT ? T : RT) * H * sizeof(uint16_t);  // <= 64 KB
+    auto* yy = static_cast<const uint16_t*>(y);
+    if (wg_is_f32)
+      router_rows_kernel<true><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E);
+    else
+      router_rows_kernel<false><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E);
+    GLM52_RETURN_LAUNCH();
+  }
+  if (stride_we != 1 || stride_wk < E || (stride_wk % vec)) return GLM52_EINVAL;
+  const int64_t stride_wg = stride_wk;
+  const int ks = choose_ks(T, H);
+  *ks_out = ks;
+  if (T == 0) return GLM52_OK;
+  if (ks > 1 && (!workspace || workspace_bytes < glm52_router_workspace_bytes(T, H, E)))
+    return GLM52_EINVAL;
+  dim3 grid((T + TB - 1) / TB, ks);
+  auto* yy = static_cast<const uint16_t*>(y);
+  auto* part = static_cast<double*>(workspace);
+  if (wg_is_f32)
+    router_logits_kernel<true><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E);
+  else
+    router_logits_kernel<false><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E);
+  GLM52_RETURN_LAUNCH();
+}
 }  // namespace
 
 extern "C" int glm52_router_logits(const void* y, int64_t stride_y, const void* wgt,
-                                   int64_t stride_wg, int wg_is_f32, float* logits,
-                                   int64_t stride_l, int T, int H, int E, hipStream_t stream) {
-  if (T < 0 || H <= 0 || E <= 0 || E > 256 || (H % (4 * KC)) != 0) return GLM52_EINVAL;
-  if (T == 0) return GLM52_OK;
-  if (!y || !wgt || !logits || stride_wg < E || stride_l < E || stride_y < H) return GLM52_EINVAL;
-  auto* yy = static_cast<const uint16_t*>(y);
-  dim3 block(256);
-  if (T <= 2) {
-    dim3 grid((T + 0) / 1, (E + kWave - 1) / kWave);
-    if (wg_is_f32)
-      router_logits_kernel<1, true><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-    else
-      router_logits_kernel<1, false><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-  } else if (T <= 64) {
-    dim3 grid((T + 3) / 4, (E + kWave - 1) / kWave);
-    if (wg_is_f32)
-      router_logits_kernel<4, true><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-    else
-      router_logits_kernel<4, false><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-  } else {
-    dim3 grid((T + 15) / 16, (E + kWave - 1) / kWave);
-    if (wg_is_f32)
-      router_logits_kernel<16, true><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-    else
-      router_logits_kernel<16, false><<<grid, block, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, T, H, E);
-  }
+                                   int64_t stride_wk, int64_t stride_we, int wg_is_f32,
+                                   float* logits, int64_t stride_l, void* workspace,
+                                   int64_t workspace_bytes, int T, int H, int E,
+                                   hipStream_t stream) {
+  int ks = 1;
+  int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                         workspace, workspace_bytes, T, H, E, &ks, stream);
+  if (rc != GLM52_OK || T == 0 || ks == 1) return rc;
+  const int64_t n = (int64_t)T * E;
+  router_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      static_cast<const double*>(workspace), logits, stride_l, T, E, ks);
   GLM52_RETURN_LAUNCH();
 }
 
@@ -209,12 +328,33 @@ extern "C" int glm52_router_topk(const float* logits, int64_t stride_l, const fl
                                  float* topw, int64_t stride_w, int32_t* topi,
                                  int64_t stride_i, int T, int E, int topk, float scale,
                                  int norm_prob, hipStream_t stream) {
-  if (T < 0 || E <= 0 || E > 256 || topk <= 0 || topk > 8 || topk > E) return GLM52_EINVAL;
+  if (T < 0 || E <= 0 || E > EMAX || (E % 4) != 0 || topk <= 0 || topk > 8 || topk > E)
+    return GLM52_EINVAL;
   if (T == 0) return GLM52_OK;
   if (!logits || !topw || !topi || stride_l < E || stride_w < topk || stride_i < topk)
     return GLM52_EINVAL;
-  dim3 grid((T + 3) / 4);
-  router_topk_kernel<<<grid, 256, 0, stream>>>(logits, stride_l, bias, topw, stride_w, topi,
-                                               stride_i, T, E, topk, scale, norm_prob);
+  router_topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(const_cast<float*>(logits), stride_l,
+                                                      nullptr, 1, bias, topw, stride_w, topi,
+                                                      stride_i, T, E, topk, scale, norm_prob);
+  GLM52_RETURN_LAUNCH();
+}
+
+// Logits + top-k in two launches (the split-K partials are reduced inside top-k).
+extern "C" int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                            int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                            void* workspace, int64_t workspace_bytes, const float* bias,
+                            float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i, int T,
+                            int H, int E, int topk, float scale, int norm_prob,
+                            hipStream_t stream) {
+  if (topk <= 0 || topk > 8 || topk > E || (E % 4) != 0 || !topw || !topi || stride_w < topk ||
+      stride_i < topk)
+    return GLM52_EINVAL;
+  int ks = 1;
+  int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                         workspace, workspace_bytes, T, H, E, &ks, stream);
+  if (rc != GLM52_OK || T == 0) return rc;
+  router_topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(
+      logits, stride_l, ks > 1 ? static_cast<const double*>(workspace) : nullptr, ks, bias,
+      topw, stride_w, topi, stride_i, T, E, topk, scale, norm_prob);
   GLM52_RETURN_LAUNCH();
 }

@@ -53,3 +53,23 @@ def moe_align_block_size(topk_ids: torch.Tensor, block_m: int, num_experts: int,
         total = int(ntp.item())
         return sti[:total].clone(), eids[: total // block_m].clone(), ntp
     return sti, eids, ntp
+
+
+def topk_align_into(logits, topw, topi, cfg, block_m, num_experts, sorted_token_ids, expert_ids,
+                    num_tokens_post_padded):
+    """Decode fast path: the router's sigmoid + biased top-k (as `topk_only`) and the
+    dispatch layout in one single-workgroup launch.  Needs T * top_k <= 256."""
+    bias = cfg.get("correction_bias")
+    _lib.require_gpu(logits, topw, topi, bias, sorted_token_ids, expert_ids,
+                     num_tokens_post_padded)
+    T, E = logits.shape
+    cap = sorted_token_ids.numel()
+    if expert_ids.numel() * block_m != cap:
+        raise ValueError("expert_ids must hold capacity / block_m entries")
+    _lib.call(
+        "glm52_router_topk_align", _lib.ptr(logits), logits.stride(0), _lib.ptr(bias),
+        _lib.ptr(topw), topw.stride(0), _lib.ptr(topi), topi.stride(0), T, E, topi.shape[1],
+        float(cfg.get("scale", 2.5)), int(bool(cfg.get("NORM_PROB", True))), int(block_m), cap,
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded),
+        _lib.stream(),
+    )

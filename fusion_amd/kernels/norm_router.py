@@ -32,17 +32,61 @@ def wgt_from_gate(gate_w: torch.Tensor) -> torch.Tensor:
     return gate_w.t().contiguous()
 
 
-def router_gemm(x2, wgt, logits, cfg):
+def workspace_bytes(T: int, H: int = HIDDEN, E: int = NUM_EXPERTS) -> int:
+    """Bytes of fp64 split-K partials the [H, E]-contiguous mapping needs at T tokens
+    (0 when K is not split; the transposed-gate mapping needs none)."""
+    return int(_lib.query("glm52_router_workspace_bytes", T, H, E))
+
+
+def _workspace(T, H, E, device, cfg, wgt=None):
+    need = 0 if (wgt is not None and wgt.stride(0) == 1) else workspace_bytes(T, H, E)
+    ws = cfg.get("workspace")
+    if need and (ws is None or ws.numel() * ws.element_size() < need):
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+    return ws, need
+
+
+def _check_router_operands(x2, wgt, logits):
+    """`wgt` is [H, E]: either contiguous (the reference's kernel layout, read by the fp64
+    MFMA mapping) or the transposed view of a contiguous [E, H] gate (`gate.t()`, read
+    one expert row per wave -- the fast mapping at decode)."""
     _lib.require_gpu(x2, wgt, logits)
     if wgt.dtype not in (torch.bfloat16, torch.float32):
         raise ValueError("router weight must be bf16 or fp32")
-    if x2.stride(-1) != 1 or wgt.stride(-1) != 1 or logits.stride(-1) != 1:
+    if x2.stride(-1) != 1 or logits.stride(-1) != 1:
         raise ValueError("router operands must be contiguous along their last dim")
+    if wgt.stride(1) != 1 and wgt.stride(0) != 1:
+        raise ValueError("router weight must be [H, E] contiguous or a transposed [E, H] gate")
+
+
+def router_gemm(x2, wgt, logits, cfg):
+    """logits[T, E] fp32 = x2 . wgt; `cfg["workspace"]` may hold the split-K scratch."""
+    _check_router_operands(x2, wgt, logits)
     T, H = x2.shape
     E = wgt.shape[1]
+    ws, need = _workspace(T, H, E, x2.device, cfg, wgt)
     _lib.call(
         "glm52_router_logits", _lib.ptr(x2), x2.stride(0), _lib.ptr(wgt), wgt.stride(0),
-        int(wgt.dtype == torch.float32), _lib.ptr(logits), logits.stride(0), T, H, E,
+        wgt.stride(1), int(wgt.dtype == torch.float32), _lib.ptr(logits), logits.stride(0),
+        _lib.ptr(ws), need, T, H, E, _lib.stream(),
+    )
+
+
+def router(x2, wgt, logits, topw, topi, cfg):
+    """router_gemm + topk_only in two launches (split-K partials reduced inside top-k)."""
+    _check_router_operands(x2, wgt, logits)
+    _lib.require_gpu(topw, topi)
+    bias = cfg.get("correction_bias")
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
+        raise ValueError("correction_bias must be a contiguous fp32 tensor")
+    T, H = x2.shape
+    E = wgt.shape[1]
+    ws, need = _workspace(T, H, E, x2.device, cfg, wgt)
+    _lib.call(
+        "glm52_router", _lib.ptr(x2), x2.stride(0), _lib.ptr(wgt), wgt.stride(0), wgt.stride(1),
+        int(wgt.dtype == torch.float32), _lib.ptr(logits), logits.stride(0), _lib.ptr(ws), need,
+        _lib.ptr(bias), _lib.ptr(topw), topw.stride(0), _lib.ptr(topi), topi.stride(0), T, H, E,
+        topi.shape[1], float(cfg.get("scale", 2.5)), int(bool(cfg.get("NORM_PROB", True))),
         _lib.stream(),
     )
 

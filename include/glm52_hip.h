@@ -33,12 +33,30 @@ int glm52_add_rmsnorm(const void* x, const void* res, const void* w, void* h1, v
                       int T, int N, float eps, int do_add, int do_norm, int rows_per_wave_mode,
                       hipStream_t stream);
 
-/* Router logits [T, E] fp32 = y [T, H] bf16 . wgt [H, E] (bf16, or fp32 if wg_is_f32),
- * fp64-accumulated and rounded once.  Replaces norm_router.router_gemm
- * (glm52/kernels/norm_router.py:347-349).  E <= 256, H % 128 == 0. */
-int glm52_router_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wg,
-                        int wg_is_f32, float* logits, int64_t stride_l, int T, int H, int E,
+/* Router logits [T, E] fp32 = y [T, H] bf16 . wgt (bf16, or fp32 if wg_is_f32), the
+ * products summed in fp64 and rounded once.  Replaces norm_router.router_gemm
+ * (glm52/kernels/norm_router.py:347-349).  wgt is addressed wgt[k * stride_wk + e * stride_we]:
+ *   stride_we == 1: the reference's [H, E] layout, read by the fp64 MFMA mapping; small T
+ *     splits K and needs a workspace of glm52_router_workspace_bytes(T, H, E) bytes;
+ *   stride_wk == 1: gate rows [E, H], one wave per expert row; no workspace.
+ * E <= 256, E % 16 == 0, H % 32 == 0, H <= 8192; wgt 16-byte aligned. */
+int glm52_router_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                        int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                        void* workspace, int64_t workspace_bytes, int T, int H, int E,
                         hipStream_t stream);
+
+/* Split-K scratch the router needs at T tokens (bytes).  No counterpart in the reference,
+ * whose Triton router sizes its grid on the host. */
+int64_t glm52_router_workspace_bytes(int T, int H, int E);
+
+/* glm52_router_logits followed by glm52_router_topk in two launches, the split-K
+ * reduction folded into the top-k pass.  Replaces the router_gemm + topk_only pair the
+ * reference chain launches (glm52/bench/bench_layer.py:426-428). */
+int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                 int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                 void* workspace, int64_t workspace_bytes, const float* bias, float* topw,
+                 int64_t stride_w, int32_t* topi, int64_t stride_i, int T, int H, int E,
+                 int topk, float scale, int norm_prob, hipStream_t stream);
 
 /* Sigmoid + noaux_tc top-k with optional correction bias (nullable), renormalisation and
  * scaling.  Replaces norm_router.topk_only (glm52/kernels/norm_router.py:352-354) with
@@ -53,6 +71,15 @@ int glm52_router_topk(const float* logits, int64_t stride_l, const float* bias, 
 int glm52_moe_align(const int32_t* topk_ids, int numel, int block_m, int num_experts,
                     int capacity, int32_t* sorted_token_ids, int32_t* expert_ids,
                     int32_t* num_tokens_post_padded, hipStream_t stream);
+
+/* glm52_router_topk followed by glm52_moe_align in one single-workgroup launch, for
+ * decode (T * topk <= 256).  Replaces the topk_only + moe_align_block_size pair
+ * (glm52/kernels/norm_router.py:352-354, glm52/reference.py:85-128). */
+int glm52_router_topk_align(const float* logits, int64_t stride_l, const float* bias, float* topw,
+                            int64_t stride_w, int32_t* topi, int64_t stride_i, int T, int E,
+                            int topk, float scale, int norm_prob, int block_m, int capacity,
+                            int32_t* sorted_token_ids, int32_t* expert_ids,
+                            int32_t* num_tokens_post_padded, hipStream_t stream);
 
 /* Grouped expert GEMM on bf16 MFMA.  Replaces moe_gateup.launch_gateup
  * (glm52/kernels/moe_gateup.py:199-248; gated = fused SwiGLU, gate_up_offset = I) and
@@ -96,8 +123,9 @@ int glm52_block_merge(const void* y, int64_t stride_yt, int64_t stride_yk, const
                       int64_t stride_h, const void* shared_out, int64_t stride_s, void* out,
                       int64_t stride_o, int T, int N, hipStream_t stream);
 
-/* Self-test of the MFMA result layout the GEMMs assume: writes a 16 x 16 fp32 matrix
- * whose row r is all (r + 1).  No counterpart in the reference. */
+/* Self-test of the MFMA result layouts the kernels assume (bf16 16x16x32 and fp64
+ * 16x16x4): writes two 16 x 16 fp32 matrices (512 floats) whose row r is all (r + 1).
+ * No counterpart in the reference. */
 int glm52_selftest_mfma_layout(float* out, hipStream_t stream);
 
 #ifdef __cplusplus

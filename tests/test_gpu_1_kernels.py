@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from fusion_amd import _lib
-from fusion_amd.dispatch import capacity, moe_align_block_size
+from fusion_amd.dispatch import capacity, moe_align_block_size, topk_align_into
 from fusion_amd.kernels import add_rmsnorm as KN
 from fusion_amd.kernels import merge_resadd as KM
 from fusion_amd.kernels import moe_down_merge as KD
@@ -36,11 +36,12 @@ def say(*a):
 
 # ------------------------------------------------------------------ MFMA layout
 def test_mfma_layout_selftest(gpu):
-    out = torch.zeros(256, dtype=torch.float32, device=gpu)
+    out = torch.zeros(512, dtype=torch.float32, device=gpu)
     _lib.call("glm52_selftest_mfma_layout", _lib.ptr(out), _lib.stream())
-    m = out.view(16, 16).cpu()
+    m = out.view(2, 16, 16).cpu()
     want = torch.arange(1, 17, dtype=torch.float32).unsqueeze(1).expand(16, 16)
-    assert torch.equal(m, want), m
+    assert torch.equal(m[0], want), m[0]
+    assert torch.equal(m[1], want), m[1]
 
 
 # ------------------------------------------------------------------ ResAdd + RMSNorm
@@ -87,7 +88,7 @@ def test_add_rmsnorm_strided_rows(gpu):
 
 
 # ------------------------------------------------------------------ router
-@pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (32, "normal"),
+@pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (13, "zipf"), (32, "normal"),
                                     (100, "zero"), (2048, "normal"), (2048, "zipf")])
 def test_router_bitwise(gpu, T, bias):
     say(f"router T={T} bias={bias}")
@@ -107,6 +108,32 @@ def test_router_bitwise(gpu, T, bias):
     w_o, ids_o, _ = O.router_select(lg_o, None if b is None else b.numpy(), 8)
     assert np.array_equal(topi.cpu().numpy(), ids_o)
     assert np.array_equal(topw.cpu().numpy(), w_o)
+    # the two-launch router (split-K partials reduced inside top-k) gives the same bits
+    cfg = {"correction_bias": None if b is None else b.to(gpu)}
+    lg2 = torch.full_like(logits, float("nan"))
+    topw2, topi2 = torch.empty_like(topw), torch.empty_like(topi)
+    KR.router(y, wgt, lg2, topw2, topi2, cfg)
+    assert torch.equal(lg2, logits) and torch.equal(topw2, topw) and torch.equal(topi2, topi)
+    # the transposed-gate mapping (a wave per gate row) gives the same bits
+    rows = fe.gate.to(gpu).t()  # [H, E] view of the contiguous [E, H] gate
+    lg3 = torch.full_like(logits, float("nan"))
+    KR.router_gemm(y, rows, lg3, {})
+    assert torch.equal(lg3, logits)
+    if T * 8 <= 256:  # the fused top-k + layout launch
+        for bm in (16, 64):
+            cap = capacity(T * 8, bm, 256)
+            sti = torch.empty(cap, dtype=torch.int32, device=gpu)
+            eids = torch.empty(cap // bm, dtype=torch.int32, device=gpu)
+            ntp = torch.empty(1, dtype=torch.int32, device=gpu)
+            topw4, topi4 = torch.empty_like(topw), torch.empty_like(topi)
+            topk_align_into(logits, topw4, topi4, cfg, bm, 256, sti, eids, ntp)
+            assert torch.equal(topw4, topw) and torch.equal(topi4, topi)
+            rs, re_, rn = O.moe_align_block_size(ids_o, bm, 256)
+            n = int(rn[0])
+            assert int(ntp.item()) == n
+            assert np.array_equal(sti.cpu().numpy()[:n], rs)
+            assert np.array_equal(eids.cpu().numpy()[: n // bm], re_)
+            assert (sti.cpu().numpy()[n:] == T * 8).all() and (eids.cpu().numpy()[n // bm:] == -1).all()
 
 
 def test_router_golden_config0(gpu):

@@ -16,11 +16,19 @@ ROOT = Path(__file__).resolve().parent.parent
 
 def declared_symbols() -> list[str]:
     hdr = (ROOT / "include" / "glm52_hip.h").read_text()
-    return sorted(set(re.findall(r"^int (glm52_\w+)\(", hdr, flags=re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t) (glm52_\w+)\(", hdr, flags=re.M)))
 
 
 def test_header_declares_every_binding():
-    assert declared_symbols() == sorted(_lib.SIGNATURES)
+    assert declared_symbols() == sorted(list(_lib.SIGNATURES) + list(_lib.QUERIES))
+
+
+def test_router_workspace_query():
+    from fusion_amd.kernels import norm_router as KR
+
+    assert KR.workspace_bytes(1) > 0  # decode splits K
+    assert KR.workspace_bytes(8192) == 0  # prefill covers the chip without a split
+    assert KR.workspace_bytes(256) == 8 * 256 * 256 * 8  # 16 token blocks x 8 K slices
 
 
 def test_library_exports_every_declared_symbol():
