@@ -42,6 +42,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--json-out", default="")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="only measure the read-bandwidth ceiling (glm52_stream_read) and exit")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="first run a plain 256 MiB device copy three times: the known-size "
+                         "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     return ap.parse_args()
 
 
@@ -65,6 +70,17 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.calibrate:
+        print(json.dumps({"calibration": calibrate(dev)}), flush=True)
+        return 0
+    if args.copy_probe:
+        src = torch.ones(2 ** 26, dtype=torch.int32, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy probe: 3 x 256 MiB device copies")
+        del src, dst
     t0 = time.time()
     W = expert_weights(device=dev)
     torch.cuda.synchronize()
@@ -178,6 +194,38 @@ def main() -> int:
     if args.json_out:
         Path(args.json_out).write_text(s + "\n")
     return 0
+
+
+def calibrate(dev) -> list:
+    """Read-bandwidth ceiling: median of 5 runs of `glm52_stream_read` per (size, load
+    kind, grid), each after a 1 GiB flush, timed with events on torch's stream."""
+    import torch
+
+    from fusion_amd import _lib
+
+    buf = torch.ones(4_000_000_000 // 4, dtype=torch.int32, device=dev)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)
+    out = []
+    for nbytes in (400_000_000, 4_000_000_000):
+        for nt in (0, 1):
+            for grid in (2048, 8192, 16384):
+                ms = []
+                for _ in range(6):
+                    flush_buf.zero_()
+                    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    s.record()
+                    _lib.call("glm52_stream_read", _lib.ptr(buf), nbytes, nt, grid, _lib.ptr(sink),
+                              _lib.stream())
+                    e.record()
+                    torch.cuda.synchronize()
+                    ms.append(s.elapsed_time(e))
+                med = statistics.median(ms[1:])
+                rec = {"bytes": nbytes, "nontemporal": bool(nt), "grid": grid,
+                       "us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
+                log(rec)
+                out.append(rec)
+    return out
 
 
 def cpu_baseline(W, T: int, seconds: float) -> dict:

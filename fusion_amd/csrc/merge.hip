@@ -296,3 +296,55 @@ extern "C" int glm52_block_merge(const void* y, int64_t stride_yt, int64_t strid
     block_merge_kernel<false><<<g, kBlock, 0, stream>>>(yy, stride_yt, stride_yk, hh, stride_h, ss, stride_s, oo, stride_o, T, N);
   GLM52_RETURN_LAUNCH();
 }
+
+// ------------------------------------------------------------------------------------
+// Read-bandwidth probe: grid-stride 16-byte loads over `bytes` of device memory, U = 4
+// loads in flight per lane, normal or non-temporal.  It measures the HBM ceiling the
+// weight-streaming kernels are held to; `sink` is written only if the xor of all words
+// equals a magic value (never, for a real buffer), which keeps the loads alive.
+// ------------------------------------------------------------------------------------
+namespace {
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+template <bool NT>
+__global__ __launch_bounds__(kBlock) void stream_read_kernel(const uint4* __restrict__ p,
+                                                             int64_t n16,
+                                                             uint32_t* __restrict__ sink) {
+  constexpr int U = 4;
+  uint32_t acc = 0;
+  const int64_t stride = (int64_t)gridDim.x * kBlock;
+  int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+  for (; i + (U - 1) * stride < n16; i += U * stride) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (NT) {
+        const u32x4_t t = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + i + u * stride));
+        v[u] = make_uint4(t[0], t[1], t[2], t[3]);
+      } else {
+        v[u] = p[i + u * stride];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (; i < n16; i += stride) {
+    const uint4 v = p[i];
+    acc ^= v.x ^ v.y ^ v.z ^ v.w;
+  }
+  if (acc == 0x9e3779b9u) sink[0] = acc;
+}
+}  // namespace
+
+extern "C" int glm52_stream_read(const void* buf, int64_t bytes, int nontemporal, int grid,
+                                 uint32_t* sink, hipStream_t stream) {
+  if (!buf || !sink || bytes < 0 || (bytes % 16) || !al16(buf) || grid <= 0 || grid > 65536)
+    return GLM52_EINVAL;
+  if (bytes == 0) return GLM52_OK;
+  auto* p = static_cast<const uint4*>(buf);
+  if (nontemporal)
+    stream_read_kernel<true><<<grid, kBlock, 0, stream>>>(p, bytes / 16, sink);
+  else
+    stream_read_kernel<false><<<grid, kBlock, 0, stream>>>(p, bytes / 16, sink);
+  GLM52_RETURN_LAUNCH();
+}

@@ -123,6 +123,13 @@ int glm52_block_merge(const void* y, int64_t stride_yt, int64_t stride_yk, const
                       int64_t stride_h, const void* shared_out, int64_t stride_s, void* out,
                       int64_t stride_o, int T, int N, hipStream_t stream);
 
+/* Read-bandwidth probe: streams `bytes` (a multiple of 16) of `buf` with 16-byte loads
+ * (non-temporal if `nontemporal`) on `grid` workgroups of 256.  It calibrates the HBM
+ * ceiling, following the reference's rule of measured ceilings (glm52/traffic.py:70-81).
+ * It replaces no launcher of the reference's kernel API. */
+int glm52_stream_read(const void* buf, int64_t bytes, int nontemporal, int grid, uint32_t* sink,
+                      hipStream_t stream);
+
 /* Self-test of the MFMA result layouts the kernels assume (bf16 16x16x32 and fp64
  * 16x16x4): writes two 16 x 16 fp32 matrices (512 floats) whose row r is all (r + 1).
  * No counterpart in the reference. */
