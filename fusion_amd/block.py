@@ -36,13 +36,21 @@ BF16 = torch.bfloat16
 
 def default_block_m(T: int) -> int:
     """Layout block size per regime: 16-row slices stream weights while each expert sees
-    a handful of rows; LDS-tiled blocks once rows per expert reach the tens."""
+    a handful of rows; 64- or 128-row blocks of the wide LDS-tiled mapping once rows per
+    expert reach the tens, so each expert's W is fetched by as few blocks as possible."""
     rows_per_expert = T * C.TOPK / C.E
-    if rows_per_expert <= 16:
+    if rows_per_expert <= 12:
         return 16
-    if rows_per_expert <= 96:
+    if rows_per_expert <= 48:
         return 64
     return 128
+
+
+def default_shared_block_m(T: int) -> int:
+    """Block size of the shared expert's one-expert layout over T rows."""
+    if T <= 12:
+        return 16
+    return 64 if T <= 512 else 128
 
 
 def shared_layout(T: int, block_m: int, device) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
@@ -75,7 +83,7 @@ class MoEBlock:
         self.w2s = w2s if w2s.dim() == 3 else w2s.unsqueeze(0)
         self.eps, self.scale = eps, scale
         self.bm = block_m or default_block_m(T)
-        self.sbm = shared_block_m or (16 if T <= 64 else (64 if T <= 1024 else 128))
+        self.sbm = shared_block_m or default_shared_block_m(T)
         self.variant = variant
 
         H, I, E, R = self.H, self.I, self.E, T * self.topk

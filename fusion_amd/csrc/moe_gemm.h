@@ -1,0 +1,50 @@
+// Pieces shared by the grouped expert GEMM kernels (moe_gemm.hip, moe_gemm_wide.hip).
+#pragma once
+
+#include "common.h"
+
+namespace glm52 {
+
+// C(16 x 16, fp32) += A(16 x 32) . B(32 x 16) on bf16 MFMA.  Lane l supplies row l % 16 of
+// A and column l % 16 of B, each as the 8 consecutive k starting at 8 (l / 16); the result
+// register i of lane l is row 4 (l / 16) + i, column l % 16.
+GLM52_DEV floatx4_t mfma16(const uint4& a, const uint4& b, floatx4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
+GLM52_DEV uint4 ldg(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
+
+struct GemmArgs {
+  const uint16_t* A;
+  int64_t sam;
+  int a_div;
+  const uint16_t* W;
+  int64_t swe;
+  int64_t swn;
+  int gu_off;  // row offset of the `up` half inside W[e] (gated only)
+  uint16_t* C;
+  int64_t scm;
+  const float* topw;  // per flat token (weighted only)
+  const int32_t* sti;
+  const int32_t* eids;
+  const int32_t* ntp;
+  int BM;  // block size of the layout
+  int n_out;
+  int K;
+  int num_valid;
+  int group_m;  // tiled mapping: row blocks per swizzle group
+  int stage_k;  // wide mapping: k per LDS stage (64: three-buffer ring, 32: four-buffer ring)
+};
+
+// The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
+// returns GLM52_EUNSUPPORTED for a block size or shape it has no instance for.
+int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
+
+}  // namespace glm52

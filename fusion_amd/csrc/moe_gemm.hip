@@ -31,45 +31,11 @@
 // Both kernels are persistent: the grid is sized on the host for the worst-case layout
 // and every workgroup loops over the items that exist for the layout the device holds
 // (`num_tokens_post_padded` is read on the device), so no host sync is needed.
-#include "common.h"
+#include "moe_gemm.h"
 
 using namespace glm52;
 
 namespace {
-
-GLM52_DEV floatx4_t mfma16(const uint4& a, const uint4& b, floatx4_t c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
-}
-
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
-  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-  return make_uint4(v[0], v[1], v[2], v[3]);
-}
-
-GLM52_DEV uint4 ldg(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
-
-struct GemmArgs {
-  const uint16_t* A;
-  int64_t sam;
-  int a_div;
-  const uint16_t* W;
-  int64_t swe;
-  int64_t swn;
-  int gu_off;  // row offset of the `up` half inside W[e] (gated only)
-  uint16_t* C;
-  int64_t scm;
-  const float* topw;  // per flat token (weighted only)
-  const int32_t* sti;
-  const int32_t* eids;
-  const int32_t* ntp;
-  int BM;  // block size of the layout
-  int n_out;
-  int K;
-  int num_valid;
-  int group_m;  // tiled mapping: row blocks per swizzle group
-};
 
 // ------------------------------------------------------------------------------------
 // stream mapping
@@ -386,7 +352,9 @@ bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
 }  // namespace
 
-// variant: 0 = choose (stream when BM == 16, tiled otherwise), 1 = stream, 2 = tiled.
+// variant: 0 = choose (stream when BM == 16, wide when BM is 64 or 128, tiled otherwise),
+// 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages
+// (moe_gemm_wide.hip; block_m in {64, 128}).
 extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                               int64_t stride_we, int64_t stride_wn, int gate_up_offset,
                               void* c, int64_t stride_cm, const float* topk_weights,
@@ -406,8 +374,13 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
   GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
              static_cast<const uint16_t*>(w), stride_we, stride_wn, gate_up_offset,
              static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
-             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4};
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64};
   const bool weighted = topk_weights != nullptr;
+  const bool auto_wide = variant == 0 && (block_m == 64 || block_m == 128);
+  if (variant == 3 || variant == 4 || auto_wide) {
+    g.stage_k = variant == 4 ? 32 : 64;
+    return launch_wide(g, capacity, gated != 0, weighted, stream);
+  }
   const bool use_stream = variant == 1 || (variant == 0 && block_m == 16);
   if (use_stream) {
     if (gated) return weighted ? launch_stream<true, true>(g, capacity, stream)

@@ -1,0 +1,327 @@
+// LDS-tiled grouped expert GEMM for prefill (tens to thousands of rows per expert),
+// gfx950.  Same semantics as the other mappings of `glm52_moe_gemm` (moe_gemm.hip):
+// `moe_gateup_kernel` (`glm52/kernels/moe_gateup.py:34-148`) when gated and
+// `moe_down_kernel` with MUL_ROUTED_WEIGHT (`glm52/kernels/moe_down_merge.py:66-169`) when
+// weighted.
+//
+// Tile.  A workgroup owns one layout block of MT rows (tokens) of one expert and 256 rows
+// of that expert's W:
+//   gated: 128 `gate` rows n0 .. n0+127 and the matching 128 `up` rows -> 128 outputs;
+//   plain: 256 rows n0 .. n0+255 -> 256 outputs.
+// Four waves split the tile 2 x 2: wave (wn, wm) computes 128 W rows x MT/2 tokens with
+// `v_mfma_f32_16x16x32_bf16`, W as the MFMA's first operand and the token rows as its
+// second, so that a lane's four results of one 16 x 16 block are four consecutive output
+// columns of one token.
+//
+// Output stores.  Inside each 32-row group of the W tile, LDS row 16 h + 4 g + i holds W
+// row 8 g + 4 h + i (h < 2, g < 4, i < 4).  Then lane (g, c) holds, in the blocks h = 0
+// and h = 1 of a group, the eight consecutive outputs 8 g .. 8 g + 7 of token c, which it
+// writes with one 16-byte store.  A gated tile keeps `gate` row n and `up` row n in the
+// same lane and register, so SwiGLU is applied in registers.
+//
+// Padding.  Real tokens fill a prefix of every layout block; 16-token groups past it are
+// neither multiplied nor stored (their A rows re-read the block's first real row).
+//
+// Order.  The kernel is persistent (one workgroup per CU).  Workgroup ids congruent
+// modulo 8 run on one XCD; each XCD takes a contiguous range of items, and the items of
+// one expert are laid out column tile major, row block fastest, so all row blocks of the
+// expert run against one W tile at the same time on one XCD: the tile is fetched from HBM
+// once and served to the others from the XCD's L2.
+#include "moe_gemm.h"
+
+using namespace glm52;
+
+namespace {
+
+constexpr int NT = 256;   // W rows per tile
+constexpr int BK = 64;    // k per LDS stage
+constexpr int LDK = BK + 8;
+constexpr int CPR = BK / 8;  // 16-byte chunks per staged row
+
+// LDS row of W row `n` (0 <= n < 32) inside its 32-row group.
+GLM52_DEV int perm32(int n) { return ((n >> 2) & 1) * 16 + (n >> 3) * 4 + (n & 3); }
+
+// ------------------------------------------------------------------------------------
+// The same tile fed by direct global -> LDS loads (`global_load_lds_dwordx4`) through a
+// ring of LDS stages (BK = 64: three stages of 64 k, two in flight while one is
+// multiplied; BK = 32: four stages of 32 k, three in flight).  No staging registers are
+// needed.  A staged row is BK bf16 (CPR 16-byte chunks); chunk c of row r is stored at
+// chunk c ^ ((r >> SW) & (CPR - 1)) with SW = log2(16 / CPR), so the 16 lanes of one
+// 128-bit operand read touch 16 distinct bank groups.  A wave's load instruction fills
+// 1 KB of LDS (64 / CPR rows) in lane order, so each lane fetches the global chunk that
+// belongs at its slot; with BK = 64 a W row is fetched 128 B at a time.
+// ------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) uint16_t lds_u16_t;
+
+// One direct 16-byte-per-lane load into LDS: lane l's 16 bytes land at byte `lds_base`
+// + 16 l (lds_base wave-uniform).  Issued from inline assembly so that the compiler's
+// wait-count pass, which loses track of these loads across the K loop's back edge and
+// would then drain every stage, leaves them alone: the kernel orders them with explicit
+// vmcnt waits before the barrier that publishes a stage.  m0 is set inside the statement
+// and nothing else in these kernels keeps a value in it.
+GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_base), "v"(gptr)
+               : "memory");
+}
+
+GLM52_DEV uint32_t lds_addr(const uint16_t* p) {
+  return (uint32_t)(uintptr_t)(const lds_u16_t*)p;
+}
+
+// s_waitcnt vmcnt(n): every older vector-memory load of this wave has completed.
+#define GLM52_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(n) : "memory")
+
+// W row (0 <= n < 32) stored at LDS row perm32(n) of its group; the inverse.
+GLM52_DEV int iperm32(int r) { return ((r >> 2) & 3) * 8 + ((r >> 4) & 1) * 4 + (r & 3); }
+
+template <int MT, int BKS, bool GATED, bool WEIGHTED>
+__global__ __launch_bounds__(256) void moe_gemm_dma_kernel(GemmArgs p) {
+  constexpr int NSTAGE = BKS == 64 ? 3 : 4;
+  constexpr int LATER = NSTAGE - 2;  // stages still in flight while one is multiplied
+  constexpr int CPR_S = BKS / 8;     // chunks per staged row
+  constexpr int SW = CPR_S == 8 ? 1 : 2;
+  constexpr int RPI = 64 / CPR_S;    // rows per load instruction
+  constexpr int TT = MT / 2;
+  constexpr int TF = TT / 16;
+  constexpr int NO = GATED ? NT / 2 : NT;
+  constexpr int WI = NT / RPI / 4;   // W load instructions per wave per stage
+  constexpr int AI = MT / RPI / 4;   // A load instructions per wave per stage
+  constexpr int IPS = WI + AI;
+  constexpr int SROWS = NT + MT;
+  static_assert(TF >= 1 && AI >= 1, "tile");
+  static_assert(LATER * IPS < 64, "vmcnt range");
+
+  // one array per stage ([W rows | A rows])
+  __shared__ __attribute__((aligned(1024))) uint16_t S0[SROWS * BKS];
+  __shared__ __attribute__((aligned(1024))) uint16_t S1[SROWS * BKS];
+  __shared__ __attribute__((aligned(1024))) uint16_t S2[SROWS * BKS];
+  __shared__ __attribute__((aligned(1024))) uint16_t S3[NSTAGE == 4 ? SROWS * BKS : 8];
+  __shared__ int toks[MT];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);
+  const int wn = wv & 1, wm = wv >> 1;
+  const int l16 = lane % 16, lg = lane / 16;
+
+  const int ntp = *p.ntp;
+  const int num_m = ntp / MT;
+  const int num_n = p.n_out / NO;
+  const int items = num_m * num_n;
+  const int nk = p.K / BKS;
+  const int per_xcd = (items + 7) / 8;
+  const int span = per_xcd * 8;
+
+  // operand reads: lane (l16, lg) reads logical chunk 4 ks + lg of row base + l16
+  int rd_off[BKS / 32];
+#pragma unroll
+  for (int ks = 0; ks < BKS / 32; ++ks)
+    rd_off[ks] = l16 * BKS + (((ks * 4 + lg) ^ ((l16 >> SW) & (CPR_S - 1))) * 8);
+  int frow[8];
+#pragma unroll
+  for (int f = 0; f < 8; ++f)
+    frow[f] = GATED ? ((f < 4) ? wn * 64 + f * 16 : 128 + wn * 64 + (f - 4) * 16)
+                    : wn * 128 + f * 16;
+
+  // load slots: lane -> row lane / CPR of the instruction's slab, physical chunk lane % CPR
+  const int dr = lane / CPR_S;
+  const int dpc = lane % CPR_S;
+
+  for (int it = blockIdx.x; it < span; it += gridDim.x) {
+    const int L = (it % 8) * per_xcd + it / 8;
+    if (L >= items) continue;
+    // Expert-aligned order: the items of expert e are [mb * num_n, (mb + cnt) * num_n)
+    // for its row blocks mb .. mb + cnt - 1, column tile major and row block fastest, so
+    // every row block of the expert runs against a W tile at the same time.
+    const int b = L / num_n;
+    const int eb = p.eids[b];
+    int mb = b, me = b + 1;
+    while (mb > 0 && p.eids[mb - 1] == eb) --mb;
+    while (me < num_m && p.eids[me] == eb) ++me;
+    const int cnt = me - mb;
+    const int local = L - mb * num_n;
+    const int pid_n = local / cnt;
+    const int pid_m = mb + local % cnt;
+    const int row0 = pid_m * MT;
+    if (p.sti[row0] >= p.num_valid) continue;
+    const int e = p.eids[pid_m];
+    const int n0 = pid_n * NO;
+
+    for (int q = tid; q < MT; q += 256) toks[q] = p.sti[row0 + q];
+    __syncthreads();
+    const int nv_rows = __builtin_amdgcn_readfirstlane(
+        __syncthreads_count(tid < MT && toks[tid] < p.num_valid));
+    const int nvf = __builtin_amdgcn_readfirstlane(max(0, min(TF, (nv_rows - wm * TT + 15) / 16)));
+
+    const uint16_t* wsrc[WI];
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const int rl = wv * (NT / 4) + i * RPI + dr;  // LDS row of the W tile
+      const int c = dpc ^ ((rl >> SW) & (CPR_S - 1));
+      int grow;
+      if (GATED) {
+        const int half = rl >> 7, within = rl & 127;
+        grow = (half ? p.gu_off : 0) + n0 + (within & ~31) + iperm32(within & 31);
+      } else {
+        grow = n0 + (rl & ~31) + iperm32(rl & 31);
+      }
+      wsrc[i] = p.W + (int64_t)e * p.swe + (int64_t)grow * p.swn + c * 8;
+    }
+    int asrc[AI];  // 32-bit element offsets into A (A holds < 2^31 elements)
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const int rl = wv * (MT / 4) + i * RPI + dr;
+      const int c = dpc ^ ((rl >> SW) & (CPR_S - 1));
+      asrc[i] = (toks[rl < nv_rows ? rl : 0] / p.a_div) * (int)p.sam + c * 8;
+    }
+
+    auto issue = [&](int kt, uint16_t* sbuf) {
+      const uint32_t wb = lds_addr(sbuf) + (uint32_t)(wvu * (NT / 4) * BKS * 2);
+      const uint32_t ab = lds_addr(sbuf + NT * BKS) + (uint32_t)(wvu * (MT / 4) * BKS * 2);
+      const int koff = kt * BKS;
+#pragma unroll
+      for (int i = 0; i < WI; ++i) dma16(wsrc[i] + koff, wb + i * 1024);
+#pragma unroll
+      for (int i = 0; i < AI; ++i) dma16(p.A + asrc[i] + koff, ab + i * 1024);
+    };
+
+    floatx4_t acc[8][TF];
+#pragma unroll
+    for (int f = 0; f < 8; ++f)
+#pragma unroll
+      for (int t = 0; t < TF; ++t) acc[f][t] = floatx4_t{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](const uint16_t* sbuf) {
+      const uint16_t* abuf = sbuf + NT * BKS;
+#pragma unroll
+      for (int ks = 0; ks < BKS / 32; ++ks) {
+        uint4 wf[8];
+#pragma unroll
+        for (int f = 0; f < 8; ++f)
+          wf[f] = *reinterpret_cast<const uint4*>(sbuf + frow[f] * BKS + rd_off[ks]);
+#pragma unroll
+        for (int t = 0; t < TF; ++t) {
+          if (t < nvf) {
+            const uint4 af = *reinterpret_cast<const uint4*>(abuf + (wm * TT + t * 16) * BKS + rd_off[ks]);
+#pragma unroll
+            for (int f = 0; f < 8; ++f) acc[f][t] = mfma16(wf[f], af, acc[f][t]);
+          }
+        }
+      }
+    };
+
+    // prologue: stages 0 .. NSTAGE - 2 in flight
+    issue(0, S0);
+    if (nk > 1) issue(1, S1);
+    if (NSTAGE == 4 && nk > 2) issue(2, S2);
+    for (int k0 = 0; k0 < nk; k0 += NSTAGE) {
+#pragma unroll
+      for (int j = 0; j < NSTAGE; ++j) {
+        const int kt = k0 + j;
+        if (kt < nk) {
+          // stage kt landed (at most LATER later stages still in flight), for all waves
+          const int later = min(LATER, nk - 1 - kt);
+          if (later >= 2) GLM52_WAIT_VMCNT(2 * IPS);
+          else if (later == 1) GLM52_WAIT_VMCNT(IPS);
+          else GLM52_WAIT_VMCNT(0);
+          __syncthreads();
+          // refill the buffer every wave finished reading before this barrier
+          const int nx = kt + NSTAGE - 1;
+          if (nx < nk) {
+            const int b = (j + NSTAGE - 1) % NSTAGE;
+            if (b == 0) issue(nx, S0);
+            if (b == 1) issue(nx, S1);
+            if (b == 2) issue(nx, S2);
+            if (NSTAGE == 4 && b == 3) issue(nx, S3);
+          }
+          if (j == 0) compute(S0);
+          if (j == 1) compute(S1);
+          if (j == 2) compute(S2);
+          if (NSTAGE == 4 && j == 3) compute(S3);
+        }
+      }
+    }
+
+#pragma unroll
+    for (int t = 0; t < TF; ++t) {
+      if (t >= nvf) continue;
+      const int tl = wm * TT + t * 16 + l16;
+      const int tok = toks[tl];
+      if (tok >= p.num_valid) continue;
+      float wgt = 1.f;
+      if (WEIGHTED) wgt = p.topw[tok];
+      uint16_t* crow = p.C + (int64_t)tok * p.scm;
+      if (GATED) {
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = silu_mul(acc[2 * pr][t][i], acc[4 + 2 * pr][t][i]);
+            v[4 + i] = silu_mul(acc[2 * pr + 1][t][i], acc[5 + 2 * pr][t][i]);
+          }
+          *reinterpret_cast<uint4*>(crow + n0 + (wn * 2 + pr) * 32 + lg * 8) = pack8(v);
+        }
+      } else {
+#pragma unroll
+        for (int pr = 0; pr < 4; ++pr) {
+          float v[8];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            v[i] = acc[2 * pr][t][i];
+            v[4 + i] = acc[2 * pr + 1][t][i];
+          }
+          if (WEIGHTED) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = v[i] * wgt;
+          }
+          *reinterpret_cast<uint4*>(crow + n0 + (wn * 4 + pr) * 32 + lg * 8) = pack8(v);
+        }
+      }
+    }
+    __syncthreads();  // toks and the ring are reused by the next item
+  }
+}
+
+template <int MT, int BKS, bool GATED, bool WEIGHTED>
+int launch_dma(const GemmArgs& a, int capacity, hipStream_t st) {
+  constexpr int NO = GATED ? NT / 2 : NT;
+  if ((a.n_out % NO) || (a.K % BKS)) return GLM52_EUNSUPPORTED;
+  const int items_max = (capacity / MT) * (a.n_out / NO);
+  int grid = items_max < 256 ? items_max : 256;
+  grid = ((grid + 7) / 8) * 8;
+  moe_gemm_dma_kernel<MT, BKS, GATED, WEIGHTED><<<grid, 256, 0, st>>>(a);
+  GLM52_RETURN_LAUNCH();
+}
+
+template <bool GATED, bool WEIGHTED>
+int launch_bm(const GemmArgs& a, int capacity, hipStream_t st) {
+  // stage_k: 64 = three-buffer ring of 64-k stages, 32 = four-buffer ring of 32-k stages
+  if (a.stage_k == 64) {
+    switch (a.BM) {
+      case 64: return launch_dma<64, 64, GATED, WEIGHTED>(a, capacity, st);
+      case 128: return launch_dma<128, 64, GATED, WEIGHTED>(a, capacity, st);
+      default: return GLM52_EUNSUPPORTED;
+    }
+  }
+  if (a.stage_k == 32) {
+    switch (a.BM) {
+      case 64: return launch_dma<64, 32, GATED, WEIGHTED>(a, capacity, st);
+      case 128: return launch_dma<128, 32, GATED, WEIGHTED>(a, capacity, st);
+      default: return GLM52_EUNSUPPORTED;
+    }
+  }
+  return GLM52_EUNSUPPORTED;
+}
+
+}  // namespace
+
+namespace glm52 {
+int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st) {
+  if (gated) return weighted ? launch_bm<true, true>(a, capacity, st) : launch_bm<true, false>(a, capacity, st);
+  return weighted ? launch_bm<false, true>(a, capacity, st) : launch_bm<false, false>(a, capacity, st);
+}
+}  // namespace glm52

@@ -11,8 +11,10 @@ conventions (`glm52/kernels/REFERENCES.md:41-51`): A rows are gathered with
   fused=False: c[f, n] = bf16(a . w13[e, n])                                ([R, 2I])
 
 `cfg["BLOCK_M"]` must equal the layout's block size (checked).  `cfg["variant"]` may
-force "stream" (weight-streaming decode mapping) or "tiled" (LDS-tiled prefill mapping);
-by default BM = 16 streams and BM in {32, 64, 128} tiles.
+force "stream" (weight-streaming decode mapping), "tiled" (register-staged LDS tiles),
+"wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages) or
+"wide32" (the same with 32-k stages); by default BM = 16 streams, BM in {64, 128} runs
+"wide" and BM = 32 "tiled".
 """
 
 from __future__ import annotations
@@ -21,7 +23,7 @@ import torch
 
 from .. import _lib
 
-VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2}
+VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4}
 
 
 def check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m: int) -> int:
@@ -64,10 +66,14 @@ def moe_gemm(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
 
 
 def smem_bytes(cfg: dict, fused: bool) -> int:
-    """LDS bytes of the tiled mapping for this cfg (the stream mapping uses 8 KB)."""
+    """LDS bytes of the mapping this cfg selects (`moe_gateup.smem_bytes`'s question)."""
     bm = cfg["BLOCK_M"]
-    if bm == 16 or cfg.get("variant") == "stream":
+    variant = cfg.get("variant")
+    if variant == "stream" or (variant is None and bm == 16):
         return 8192
+    if variant in ("wide", "wide32") or (variant is None and bm in (64, 128)):
+        stages, bk = (4, 32) if variant == "wide32" else (3, 64)
+        return stages * (256 + bm) * bk * 2 + 4 * bm
     nb = 128
     return 2 * (bm + nb) * (64 + 8) * 2 + 4 * bm
 

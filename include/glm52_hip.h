@@ -86,7 +86,9 @@ int glm52_router_topk_align(const float* logits, int64_t stride_l, const float* 
  * moe_down_merge.launch_down with fuse_merge=False (glm52/kernels/moe_down_merge.py:427-476;
  * topk_weights non-null = MUL_ROUTED_WEIGHT).  A rows are a[sorted_id / a_row_div],
  * W is [E, N, K] with K contiguous, C rows are indexed by the flat token id.
- * variant: 0 auto, 1 weight-streaming, 2 LDS-tiled (block_m in {32, 64, 128}). */
+ * variant: 0 auto, 1 weight-streaming, 2 register-staged LDS tiles (block_m in {32, 64,
+ * 128}), 3 / 4 wide 256-row W tiles fed by direct global -> LDS loads through 64-k / 32-k
+ * stages (block_m in {64, 128}); auto streams at block_m 16, runs 3 at 64 and 128. */
 int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                    int64_t stride_we, int64_t stride_wn, int gate_up_offset, void* c,
                    int64_t stride_cm, const float* topk_weights, const int32_t* sorted_token_ids,

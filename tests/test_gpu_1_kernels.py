@@ -230,7 +230,9 @@ def _close(got: torch.Tensor, ref: torch.Tensor, what: str):
 
 
 @pytest.mark.parametrize("bm,variant", [(16, "stream"), (32, "tiled"), (64, "tiled"),
-                                        (128, "tiled"), (64, "stream")])
+                                        (128, "tiled"), (64, "stream"), (64, "wide"),
+                                        (128, "wide"), (64, "wide32"), (128, "wide32"),
+                                        (128, None)])
 def test_grouped_gemms_small(gpu, bm, variant):
     say(f"grouped gemm small bm={bm} {variant}")
     T, E, H, I, k = 40, 16, 512, 256, 8
@@ -263,7 +265,8 @@ def test_grouped_gemm_full_width(gpu):
     a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 5, gpu)
     ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
     act_ref = _gateup_ref(a, w13, ids, k, I, True)
-    for bm, variant in ((16, "stream"), (32, "tiled")):
+    for bm, variant in ((16, "stream"), (32, "tiled"), (64, "wide"), (128, "wide"),
+                        (64, "wide32")):
         say(f"grouped gemm full width bm={bm} {variant}")
         sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
         cfg = {"BLOCK_M": bm, "variant": variant}

@@ -87,7 +87,11 @@ def test_shared_layout_matches_reference_rule():
 
 
 def test_default_block_m_regimes():
+    # decode streams 16-row slices; prefill uses the wide tiles' 64- and 128-row blocks
     assert block.default_block_m(1) == 16
     assert block.default_block_m(256) == 16
-    assert block.default_block_m(2048) == 64
+    assert block.default_block_m(1024) == 64
+    assert block.default_block_m(2048) == 128
     assert block.default_block_m(8192) == 128
+    assert [block.default_shared_block_m(T) for T in (1, 32, 256, 2048, 8192)] == [16, 64, 64,
+                                                                                    128, 128]
