@@ -30,8 +30,12 @@ SIGNATURES: dict[str, list] = {
                                 _P, _P],
     "glm52_router_topk": [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _F, _I, _P],
     "glm52_moe_align": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "glm52_decode_front": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L,
+                           _I, _I, _I, _I, _F, _F, _I, _I, _I, _P, _P, _P, _P, _P],
     "glm52_moe_gemm": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                        _I, _I, _P],
+    "glm52_moe_gemm_shared": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I,
+                              _P, _L, _P, _P, _L, _I, _I, _I, _I, _P],
     "glm52_silu_and_mul": [_P, _L, _P, _L, _I, _I, _P],
     "glm52_moe_sum": [_P, _L, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
     "glm52_resadd": [_P, _L, _P, _L, _P, _L, _I, _I, _P],

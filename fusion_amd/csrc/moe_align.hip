@@ -17,9 +17,10 @@
 // is graph-capturable.  Slots past the count hold the sentinel and blocks past it hold
 // expert id -1; consumers stop at `num_tokens_post_padded`.
 //
-// One workgroup builds the layout (select.h: LDS histogram, padded prefix, sentinel
-// fill, then a stable scatter that walks the ids in index order, ranking equal keys
-// inside each wave with ballots and across waves with a per-wave count table).
+// One workgroup builds the layout (select.h, align_body_waves): per-wave LDS histograms
+// over contiguous index ranges, padded prefix, sentinel fill, then a stable scatter in
+// which every wave walks its own range in index order, ranking equal keys inside each
+// 64-id step with ballots.
 //
 // For decode the router's top-k and the layout run as one launch
 // (`router_topk_align_kernel`): one workgroup selects the experts of every token, keeps
@@ -37,11 +38,10 @@ __global__ __launch_bounds__(kThreads) void moe_align_kernel(
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
     int32_t* __restrict__ ntp_out) {
   __shared__ AlignLds<kThreads> sh;
-  align_body<kThreads>(ids, numel, E, BM, capacity, sorted_ids, expert_ids, ntp_out, sh);
+  align_body_waves<kThreads>(ids, numel, E, BM, capacity, sorted_ids, expert_ids, ntp_out, sh);
 }
 
 constexpr int kFusedThreads = 256;
-constexpr int kFusedSlots = 256;  // T * topk <= 256
 
 __global__ __launch_bounds__(kFusedThreads) void router_topk_align_kernel(
     const float* __restrict__ logits, int64_t sl, const float* __restrict__ bias,
@@ -49,39 +49,11 @@ __global__ __launch_bounds__(kFusedThreads) void router_topk_align_kernel(
     int E, int topk, float scale, int norm_prob, int BM, int capacity,
     int32_t* __restrict__ sorted_ids, int32_t* __restrict__ expert_ids,
     int32_t* __restrict__ ntp_out) {
-  __shared__ float keys[4][kMaxE];
-  __shared__ float sel_s[4][8];
-  __shared__ int sel_i[4][8];
-  __shared__ int ids_s[kFusedSlots];
-  __shared__ AlignLds<kFusedThreads> sh;
-  const int lane = threadIdx.x % kWave;
-  const int wv = threadIdx.x / kWave;
-
-  for (int t0 = 0; t0 < T; t0 += 4) {
-    const int t = t0 + wv;
-    const bool active = t < T;
-    float lg[4], sc[4], key[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int e = lane + j * kWave;
-      lg[j] = (active && e < E) ? logits[(int64_t)t * sl + e] : 0.f;
-    }
-    topk_keys(lg, bias, E, active, sc, key, keys[wv]);
-    __syncthreads();
-    if (active) topk_rank(keys[wv], sc, key, E, topk, sel_s[wv], sel_i[wv]);
-    __syncthreads();
-    if (active && lane < topk) {
-      float w;
-      int id;
-      topk_weight(sel_s[wv], sel_i[wv], topk, scale, norm_prob, &w, &id);
-      topw[(int64_t)t * stw + lane] = w;
-      topi[(int64_t)t * sti + lane] = id;
-      ids_s[t * topk + lane] = id;
-    }
-    __syncthreads();
-  }
-  align_body<kFusedThreads>(ids_s, T * topk, E, BM, capacity, sorted_ids, expert_ids, ntp_out,
-                            sh);
+  __shared__ TopkAlignLds sh;
+  float bv[4];
+  load_bias(bias, E, bv);
+  topk_align_block(logits, sl, bv, bias != nullptr, topw, stw, topi, sti, T, E, topk, scale,
+                   norm_prob, BM, capacity, sorted_ids, expert_ids, ntp_out, sh);
 }
 
 int check_layout_args(int numel, int block_m, int num_experts, int capacity,
@@ -117,7 +89,7 @@ extern "C" int glm52_router_topk_align(const float* logits, int64_t stride_l, co
                                        int32_t* sorted_token_ids, int32_t* expert_ids,
                                        int32_t* num_tokens_post_padded, hipStream_t stream) {
   if (T < 0 || E <= 0 || E > kMaxE || (E % 4) != 0 || topk <= 0 || topk > 8 || topk > E ||
-      (int64_t)T * topk > kFusedSlots)
+      (int64_t)T * topk > kTopkAlignSlots)
     return GLM52_EINVAL;
   if (!logits || !topw || !topi || stride_l < E || stride_w < topk || stride_i < topk)
     return GLM52_EINVAL;

@@ -21,6 +21,17 @@ GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
 
 GLM52_DEV uint4 ldg(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3 for raw,
+// range-checked 32-bit loads): a load whose offset is out of range returns zero without
+// touching memory.
+GLM52_DEV __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+GLM52_DEV uint4 ldb(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+
 struct GemmArgs {
   const uint16_t* A;
   int64_t sam;
@@ -41,6 +52,17 @@ struct GemmArgs {
   int num_valid;
   int group_m;  // tiled mapping: row blocks per swizzle group
   int stage_k;  // wide mapping: k per LDS stage (64: three-buffer ring, 32: four-buffer ring)
+  // stream mapping: an extra expert (the shared one) whose rows are tokens 0 .. x_rows - 1
+  // of its own input Ax, with weights Wx ([N, K] like W[e]) and its own output Cx;
+  // x_rows = 0: none
+  const uint16_t* Ax;
+  int64_t sax;
+  const uint16_t* Wx;
+  uint16_t* Cx;
+  int64_t scx;
+  int x_rows;
+  int a_bytes;   // stream mapping: bytes of A (and of Ax) its token rows span
+  int ax_bytes;
 };
 
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):

@@ -20,7 +20,9 @@
 //  * stream (decode): the GEMM is a weight stream.  An item is one 16-row slice of the
 //    layout times 16 output columns; the four waves of a workgroup each take a quarter of
 //    K, load their W fragments straight from HBM into registers (128-bit non-temporal
-//    loads, U steps in flight), and meet in LDS for the split-K sum and the epilogue.
+//    loads, U steps of 64 k in flight), read the token rows through a range-checked
+//    buffer (padding rows read zeros without a memory access), and meet in LDS for the
+//    split-K sum and the epilogue.
 //
 //  * tiled (prefill): LDS-staged BM x BN tiles with a register-staged double buffer; a
 //    workgroup of four waves computes a BM x BN block with 16x16x32 MFMAs.  Items are
@@ -53,71 +55,72 @@ __global__ __launch_bounds__(256) void moe_gemm_stream_kernel(GemmArgs p) {
   const int ntp = *p.ntp;
   const int num_m = ntp / 16;
   const int num_n = p.n_out / 16;
-  const int items = num_m * num_n;
+  const int items_r = num_m * num_n;
+  const int items = items_r + ((p.x_rows + 15) / 16) * num_n;  // + the extra expert's
   const int kq = p.K / 4;
   const int kbeg = wv * kq;
 
   for (int it = blockIdx.x; it < items; it += gridDim.x) {
     // n fastest: consecutive workgroups stream different W rows of the same expert
-    const int pid_m = it / num_n;
-    const int pid_n = it % num_n;
+    const bool extra = it >= items_r;
+    const int li = extra ? it - items_r : it;
+    const int pid_m = li / num_n;
+    const int pid_n = li % num_n;
     const int row0 = pid_m * 16;
-    if (p.sti[row0] >= p.num_valid) continue;  // an all-padding slice (BM > 16)
-    const int e = p.eids[row0 / p.BM];
+    int tok;
+    bool tok_ok;
+    const uint16_t* wbase;
+    if (extra) {  // the extra expert: rows are tokens 0 .. x_rows - 1, A row = token
+      tok = row0 + r;
+      tok_ok = tok < p.x_rows;
+      wbase = p.Wx;
+    } else {
+      if (p.sti[row0] >= p.num_valid) continue;  // an all-padding slice (BM > 16)
+      tok = p.sti[row0 + r];
+      tok_ok = tok < p.num_valid;
+      wbase = p.W + (int64_t)p.eids[row0 / p.BM] * p.swe;
+    }
     const int n0 = pid_n * 16;
-
-    const int tok = p.sti[row0 + r];
-    const bool tok_ok = tok < p.num_valid;
-    const uint16_t* arow = p.A + (int64_t)(tok_ok ? tok / p.a_div : 0) * p.sam + 16 * g;
-    const uint16_t* wg = p.W + (int64_t)e * p.swe + (int64_t)(n0 + r) * p.swn + 16 * g;
+    // token rows through a range-checked buffer: padding rows read zeros at no cost
+    const __amdgpu_buffer_rsrc_t arsrc = extra ? buffer_rsrc(p.Ax, p.ax_bytes) : buffer_rsrc(p.A, p.a_bytes);
+    const uint32_t abad = (uint32_t)(extra ? p.ax_bytes : p.a_bytes);
+    const uint32_t aoff = tok_ok ? (uint32_t)(((int64_t)(extra ? tok : tok / p.a_div) *
+                                               (extra ? p.sax : p.sam) + 16 * g) * 2)
+                                 : abad;
+    const uint16_t* wg = wbase + (int64_t)(n0 + r) * p.swn + 16 * g;
     const uint16_t* wu = wg + (int64_t)p.gu_off * p.swn;
 
     floatx4_t accg = {0.f, 0.f, 0.f, 0.f};
     floatx4_t accu = {0.f, 0.f, 0.f, 0.f};
+    // U steps of 64 k in flight per lane (W: non-temporal 16-byte loads), then their MFMAs
     int k = kbeg;
     const int kend = kbeg + kq;
-    for (; k + 64 * U <= kend; k += 64 * U) {
+    for (; k < kend; k += 64 * U) {
       uint4 bg[U][2], bu[U][2], av[U][2];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kk = k + u * 64;
-        bg[u][0] = ldg_nt(wg + kk);
-        bg[u][1] = ldg_nt(wg + kk + 8);
-        if (GATED) {
-          bu[u][0] = ldg_nt(wu + kk);
-          bu[u][1] = ldg_nt(wu + kk + 8);
-        }
-        if (tok_ok) {
-          av[u][0] = ldg(arow + kk);
-          av[u][1] = ldg(arow + kk + 8);
-        } else {
-          av[u][0] = make_uint4(0, 0, 0, 0);
-          av[u][1] = make_uint4(0, 0, 0, 0);
+        if (kk < kend) {
+          bg[u][0] = ldg_nt(wg + kk);
+          bg[u][1] = ldg_nt(wg + kk + 8);
+          if (GATED) {
+            bu[u][0] = ldg_nt(wu + kk);
+            bu[u][1] = ldg_nt(wu + kk + 8);
+          }
+          av[u][0] = ldb(arsrc, aoff + kk * 2);
+          av[u][1] = ldb(arsrc, aoff + kk * 2 + 16);
         }
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        accg = mfma16(av[u][0], bg[u][0], accg);
-        accg = mfma16(av[u][1], bg[u][1], accg);
-        if (GATED) {
-          accu = mfma16(av[u][0], bu[u][0], accu);
-          accu = mfma16(av[u][1], bu[u][1], accu);
+        if (k + u * 64 < kend) {
+          accg = mfma16(av[u][0], bg[u][0], accg);
+          accg = mfma16(av[u][1], bg[u][1], accg);
+          if (GATED) {
+            accu = mfma16(av[u][0], bu[u][0], accu);
+            accu = mfma16(av[u][1], bu[u][1], accu);
+          }
         }
-      }
-    }
-    for (; k < kend; k += 64) {
-      const uint4 b0 = ldg_nt(wg + k), b1 = ldg_nt(wg + k + 8);
-      uint4 a0 = make_uint4(0, 0, 0, 0), a1 = a0;
-      if (tok_ok) {
-        a0 = ldg(arow + k);
-        a1 = ldg(arow + k + 8);
-      }
-      accg = mfma16(a0, b0, accg);
-      accg = mfma16(a1, b1, accg);
-      if (GATED) {
-        const uint4 c0 = ldg_nt(wu + k), c1 = ldg_nt(wu + k + 8);
-        accu = mfma16(a0, c0, accu);
-        accu = mfma16(a1, c1, accu);
       }
     }
 
@@ -132,7 +135,7 @@ __global__ __launch_bounds__(256) void moe_gemm_stream_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int orow = 4 * g + i;
-        const int otok = p.sti[row0 + orow];
+        const int otok = extra ? row0 + orow : p.sti[row0 + orow];
         const float sg = ((red[0][0][i][lane] + red[1][0][i][lane]) + red[2][0][i][lane]) + red[3][0][i][lane];
         float v;
         if (GATED) {
@@ -142,7 +145,9 @@ __global__ __launch_bounds__(256) void moe_gemm_stream_kernel(GemmArgs p) {
         } else {
           v = sg;
         }
-        if (otok < p.num_valid) {
+        if (extra) {
+          if (otok < p.x_rows) p.Cx[(int64_t)otok * p.scx + n0 + r] = f32_to_bf16(v);
+        } else if (otok < p.num_valid) {
           if (WEIGHTED) v = v * p.topw[otok];
           p.C[(int64_t)otok * p.scm + n0 + r] = f32_to_bf16(v);
         }
@@ -311,7 +316,7 @@ __global__ __launch_bounds__(256) void moe_gemm_tiled_kernel(GemmArgs p) {
 
 template <bool GATED, bool WEIGHTED>
 int launch_stream(const GemmArgs& a, int capacity, hipStream_t st) {
-  const int items_max = (capacity / 16) * (a.n_out / 16);
+  const int items_max = (capacity / 16 + (a.x_rows + 15) / 16) * (a.n_out / 16);
   int grid = items_max < 4096 ? items_max : 4096;
   if (grid < 1) grid = 1;
   moe_gemm_stream_kernel<GATED, WEIGHTED, 4><<<grid, 256, 0, st>>>(a);
@@ -350,6 +355,14 @@ int launch_tiled_bm(const GemmArgs& a, int capacity, hipStream_t st) {
 
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
+// Bytes spanned by the A rows a layout can address: row f / a_div of every valid flat
+// index f, each K elements long at stride sa (the buffer range of the token loads).
+int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
+  const int64_t rows = ((int64_t)num_valid + a_div - 1) / a_div;
+  const int64_t b = rows == 0 ? 0 : ((rows - 1) * sa + k) * 2;
+  return b > 0x7ffffff0 ? 0x7ffffff0 : (int)b;
+}
+
 }  // namespace
 
 // variant: 0 = choose (stream when BM == 16, wide when BM is 64 or 128, tiled otherwise),
@@ -374,7 +387,8 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
   GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
              static_cast<const uint16_t*>(w), stride_we, stride_wn, gate_up_offset,
              static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
-             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64};
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
+             nullptr, 0, nullptr, nullptr, 0, 0, a_bytes(num_valid_tokens, a_row_div, stride_am, k), 0};
   const bool weighted = topk_weights != nullptr;
   const bool auto_wide = variant == 0 && (block_m == 64 || block_m == 128);
   if (variant == 3 || variant == 4 || auto_wide) {
@@ -392,6 +406,46 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
                              : launch_tiled_bm<true, false>(g, capacity, stream);
   return weighted ? launch_tiled_bm<false, true>(g, capacity, stream)
                   : launch_tiled_bm<false, false>(g, capacity, stream);
+}
+
+// The routed grouped GEMM and the shared expert's GEMM in one weight-streaming launch
+// (decode): the shared expert is an extra expert whose rows are the tokens 0 .. T - 1 of
+// its own input (no routing weight), written to its own output.  Same operand rules as
+// glm52_moe_gemm with block_m = 16.
+extern "C" int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row_div,
+                                     const void* w, int64_t stride_we, int64_t stride_wn,
+                                     int gate_up_offset, void* c, int64_t stride_cm,
+                                     const float* topk_weights, const int32_t* sorted_token_ids,
+                                     const int32_t* expert_ids,
+                                     const int32_t* num_tokens_post_padded, int capacity,
+                                     int block_m, int num_valid_tokens, const void* a_shared,
+                                     int64_t stride_as, const void* w_shared, void* c_shared,
+                                     int64_t stride_cs, int shared_rows, int n_out, int k,
+                                     int gated, hipStream_t stream) {
+  if (!a || !w || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded ||
+      !a_shared || !w_shared || !c_shared)
+    return GLM52_EINVAL;
+  if (!al16(a_shared) || (stride_as % 8)) return GLM52_EINVAL;
+  if (block_m != 16 || capacity < 0 || (capacity % block_m) || shared_rows < 0) return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % 16) != 0 || k <= 0 || (k % 256) != 0 || a_row_div <= 0)
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w) || !al16(w_shared) || (stride_am % 8) || (stride_we % 8) ||
+      (stride_wn % 8))
+    return GLM52_EINVAL;
+  if (gated && (gate_up_offset < n_out)) return GLM52_EINVAL;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
+             static_cast<const uint16_t*>(w), stride_we, stride_wn, gate_up_offset,
+             static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
+             static_cast<const uint16_t*>(a_shared), stride_as,
+             static_cast<const uint16_t*>(w_shared), static_cast<uint16_t*>(c_shared), stride_cs,
+             shared_rows, a_bytes(num_valid_tokens, a_row_div, stride_am, k),
+             a_bytes(shared_rows, 1, stride_as, k)};
+  const bool weighted = topk_weights != nullptr;
+  if (gated) return weighted ? launch_stream<true, true>(g, capacity, stream)
+                             : launch_stream<true, false>(g, capacity, stream);
+  return weighted ? launch_stream<false, true>(g, capacity, stream)
+                  : launch_stream<false, false>(g, capacity, stream);
 }
 
 // Self-test of the MFMA result layouts this library assumes, for the bf16 16x16x32 and

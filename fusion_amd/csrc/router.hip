@@ -22,14 +22,14 @@
 // the reference kernel's layout): the logits run on the fp64 matrix cores
 // (`v_mfma_f64_16x16x4_f64`): a workgroup owns 16
 // tokens x all experts, each of its four waves 64 experts (four 16 x 16 fp64 tiles), and
-// walks a K slice staging y (as fp64) and the gate weight (as stored) in LDS.  Small T
+// walks a K slice through two LDS buffers holding y (as fp64) and the gate weight (as
+// stored), the next chunk's loads in flight while the current chunk is multiplied.  Small T
 // splits K over KS workgroups; their fp64 partials land in a caller-provided workspace
 // and are summed in a fixed order (by `router_reduce_kernel`, or inside the top-k kernel)
 // before the single rounding to fp32.
 //
-// Top-k: one wave per token.  Each expert's rank is the number of experts that beat it
-// under the (choice descending, index ascending) order; ranks form a permutation, and
-// the experts of rank < k land in slot = rank, already sorted.  No sequential rounds.
+// Top-k: one wave per token, k rounds of a wave-wide argmax under the (choice
+// descending, index ascending) order (select.h).
 //
 // The gate weight layout is the reference kernel's [H, E] (`wgt_from_gate`,
 // `glm52/kernels/norm_router.py:251-255`).
@@ -41,7 +41,7 @@ typedef double doublex4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int KC = 32;    // k rows staged per chunk
+constexpr int KC = 64;    // k granularity of the [H, E] mapping (its largest chunk)
 constexpr int TB = 16;    // tokens per workgroup (one fp64 MFMA tile)
 constexpr int EMAX = kMaxE;
 
@@ -50,13 +50,21 @@ GLM52_DEV doublex4_t mfma64(double a, double b, doublex4_t c) {
 }
 
 // grid = (ceil(T / 16), KS); block = 256.  KS == 1: fp32 logits out; else fp64 partials.
+// K advances in chunks of KC (64 for a bf16 gate, 32 for fp32) through two LDS buffers:
+// the next chunk's gate rows and token rows are loaded into registers (16-byte loads)
+// while the MFMAs consume the current chunk, then stored to the other buffer.
 template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swg,
     float* __restrict__ logits, int64_t sl, double* __restrict__ part, int T, int H, int E) {
   using WT = typename std::conditional<WG_F32, float, uint16_t>::type;
-  __shared__ double ys[TB][KC + 1];
-  __shared__ WT ws[KC][EMAX + (WG_F32 ? 4 : 8)];
+  constexpr int KCH = WG_F32 ? 32 : 64;     // k rows per chunk
+  constexpr int VEC = WG_F32 ? 4 : 8;       // gate elements per 16-byte vector
+  constexpr int GV = KCH * EMAX / VEC / 256;  // gate vectors per thread per chunk
+  constexpr int YV = TB * KCH / 8;          // 16-byte y vectors per chunk (threads 0 .. YV-1)
+  static_assert(YV <= 256 && GV >= 1, "chunk");
+  __shared__ double ys[2][TB][KCH + 1];
+  __shared__ __attribute__((aligned(16))) WT ws[2][KCH][EMAX + (WG_F32 ? 4 : 8)];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -65,35 +73,61 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   const int KS = gridDim.y;
   const int ksl = H / KS;
   const int kbeg = blockIdx.y * ksl;
+  const int nch = ksl / KCH;
   const WT* wg = static_cast<const WT*>(wg_raw);
   const int ntile = E / 16;
+  const int vpr = E / VEC;  // gate vectors per k row
+
+  uint4 rg[GV], ry;
+  auto gload = [&](int c) {
+    const int k0 = kbeg + c * KCH;
+#pragma unroll
+    for (int i = 0; i < GV; ++i) {
+      const int q = tid + i * 256;
+      const int kk = q / (EMAX / VEC), v = q % (EMAX / VEC);
+      rg[i] = v < vpr ? *reinterpret_cast<const uint4*>(wg + (int64_t)(k0 + kk) * swg + v * VEC)
+                      : make_uint4(0, 0, 0, 0);
+    }
+    if (tid < YV) {
+      const int t = tid / (KCH / 8), kc = tid % (KCH / 8);
+      ry = t0 + t < T ? *reinterpret_cast<const uint4*>(y + (int64_t)(t0 + t) * sy + k0 + kc * 8)
+                      : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto sstore = [&](int b) {
+#pragma unroll
+    for (int i = 0; i < GV; ++i) {
+      const int q = tid + i * 256;
+      const int kk = q / (EMAX / VEC), v = q % (EMAX / VEC);
+      *reinterpret_cast<uint4*>(&ws[b][kk][v * VEC]) = rg[i];
+    }
+    if (tid < YV) {
+      const int t = tid / (KCH / 8), kc = tid % (KCH / 8);
+      float f[8];
+      unpack8(ry, f);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) ys[b][t][kc * 8 + q] = (double)f[q];
+    }
+  };
 
   doublex4_t acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = doublex4_t{0.0, 0.0, 0.0, 0.0};
 
-  for (int k0 = kbeg; k0 < kbeg + ksl; k0 += KC) {
-    // stage y[t0 .. t0+16)[k0 .. k0+32) as fp64 and Wg[k0 .. k0+32)[0 .. E)
-    for (int q = tid; q < TB * KC; q += 256) {
-      const int t = q / KC, kk = q % KC;
-      ys[t][kk] = (t0 + t < T) ? (double)bf16_to_f32(y[(int64_t)(t0 + t) * sy + k0 + kk]) : 0.0;
-    }
-    constexpr int VEC = WG_F32 ? 4 : 8;  // 16-byte vectors of the gate row
-    const int vpr = E / VEC;
-    for (int q = tid; q < KC * vpr; q += 256) {
-      const int kk = q / vpr, c = q % vpr;
-      *reinterpret_cast<uint4*>(&ws[kk][c * VEC]) =
-          *reinterpret_cast<const uint4*>(wg + (int64_t)(k0 + kk) * swg + c * VEC);
-    }
-    __syncthreads();
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int cur = c & 1;
+    if (c + 1 < nch) gload(c + 1);
 #pragma unroll
-    for (int k4 = 0; k4 < KC; k4 += 4) {
-      const double a = ys[lane % 16][k4 + lane / 16];
+    for (int k4 = 0; k4 < KCH; k4 += 4) {
+      const double a = ys[cur][lane % 16][k4 + lane / 16];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int tile = wv * 4 + j;
         if (tile < ntile) {
-          const WT raw = ws[k4 + lane / 16][tile * 16 + lane % 16];
+          const WT raw = ws[cur][k4 + lane / 16][tile * 16 + lane % 16];
           double b;
           if constexpr (WG_F32) b = (double)raw;
           else b = (double)bf16_to_f32(raw);
@@ -101,6 +135,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
         }
       }
     }
+    if (c + 1 < nch) sstore(cur ^ 1);
     __syncthreads();
   }
 
@@ -206,7 +241,6 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ bias, float* __restrict__ topw, int64_t stw,
     int32_t* __restrict__ topi, int64_t sti, int T, int E, int topk, float scale,
     int norm_prob) {
-  __shared__ float keys[4][kMaxE];
   __shared__ float sel_s[4][8];
   __shared__ int sel_i[4][8];
   const int lane = threadIdx.x % kWave;
@@ -238,9 +272,10 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       }
     }
   }
-  topk_keys(lg, bias, E, t_ok, sc, key, keys[wv]);
-  __syncthreads();
-  if (t_ok) topk_rank(keys[wv], sc, key, E, topk, sel_s[wv], sel_i[wv]);
+  float bv[4];
+  load_bias(bias, E, bv);
+  topk_keys(lg, bv, bias != nullptr, E, t_ok, sc, key);
+  topk_rank(sc, key, E, t_ok ? topk : 0, sel_s[wv], sel_i[wv]);
   __syncthreads();
   if (t_ok && lane < topk) {
     float w;

@@ -73,3 +73,37 @@ def topk_align_into(logits, topw, topi, cfg, block_m, num_experts, sorted_token_
         _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded),
         _lib.stream(),
     )
+
+
+DECODE_FRONT_MAX_T = 4
+
+
+def decode_front_into(x, r, w_norm, h1, y, gate_rows, cfg, logits, topw, topi, block_m,
+                      sorted_token_ids, expert_ids, num_tokens_post_padded, counter):
+    """Decode front end in one launch (T <= 4): ResAdd + RMSNorm, router logits from the
+    contiguous [E, H] gate rows, biased top-k and the dispatch layout -- the chain
+    `fused_add_rmsnorm` -> `router_gemm` -> `topk_only` -> `moe_align_block_size`, with
+    bit-identical outputs.  `counter` is an int32 device tensor that is zero before the
+    first call and is left zero by every call."""
+    bias = cfg.get("correction_bias")
+    _lib.require_gpu(x, r, w_norm, h1, y, gate_rows, logits, topw, topi, bias,
+                     sorted_token_ids, expert_ids, num_tokens_post_padded, counter)
+    T, H = x.shape
+    E = gate_rows.shape[0]
+    if gate_rows.shape[1] != H or gate_rows.stride(1) != 1 or gate_rows.dtype != torch.bfloat16:
+        raise ValueError("gate_rows must be the contiguous [E, H] bf16 gate")
+    if counter.dtype != torch.int32:
+        raise ValueError("counter must be an int32 device tensor")
+    cap = sorted_token_ids.numel()
+    if expert_ids.numel() * block_m != cap:
+        raise ValueError("expert_ids must hold capacity / block_m entries")
+    _lib.call(
+        "glm52_decode_front", _lib.ptr(x), x.stride(0), _lib.ptr(r), r.stride(0),
+        _lib.ptr(w_norm), _lib.ptr(h1), h1.stride(0), _lib.ptr(y), y.stride(0),
+        _lib.ptr(gate_rows), gate_rows.stride(0), _lib.ptr(bias), _lib.ptr(logits),
+        logits.stride(0), _lib.ptr(topw), topw.stride(0), _lib.ptr(topi), topi.stride(0), T, H,
+        E, topi.shape[1], float(cfg.get("eps", 1e-5)), float(cfg.get("scale", 2.5)),
+        int(bool(cfg.get("NORM_PROB", True))), int(block_m), cap, _lib.ptr(sorted_token_ids),
+        _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), _lib.ptr(counter),
+        _lib.stream(),
+    )

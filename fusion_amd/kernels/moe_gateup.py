@@ -65,6 +65,38 @@ def moe_gemm(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
     )
 
 
+def moe_gemm_shared(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
+                    num_tokens_post_padded, num_valid_tokens, n_out, gate_up_offset, gated, cfg,
+                    a_shared, w_shared, c_shared):
+    """`moe_gemm` on the weight-streaming mapping with the shared expert in the same
+    launch: `w_shared` ([1, N, K] or [N, K]) is applied to every row of `a_shared`
+    (one row per token, no routing weight) and written to `c_shared`."""
+    _lib.require_gpu(a, w, c, sorted_token_ids, expert_ids, num_tokens_post_padded, topk_weights,
+                     a_shared, w_shared, c_shared)
+    for t, n in ((a, "a"), (w, "w"), (c, "c"), (a_shared, "a_shared"), (w_shared, "w_shared"),
+                 (c_shared, "c_shared")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be bf16 and contiguous along its last dim")
+    ws = w_shared[0] if w_shared.dim() == 3 else w_shared
+    if ws.shape[1:] != w.shape[2:] or ws.stride(0) != w.stride(1) or ws.shape[0] != w.shape[1]:
+        raise ValueError("w_shared must have the routed experts' [N, K] shape and row stride")
+    if a_shared.shape[1] != a.shape[1] or c_shared.shape[0] != a_shared.shape[0]:
+        raise ValueError("a_shared / c_shared rows must match (one per token)")
+    bm = int(cfg["BLOCK_M"])
+    if bm != 16:
+        raise ValueError("the fused shared-expert launch streams weights: BLOCK_M must be 16")
+    cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    K = a.shape[1]
+    _lib.call(
+        "glm52_moe_gemm_shared", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w), w.stride(0),
+        w.stride(1), int(gate_up_offset), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights),
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), cap,
+        bm, int(num_valid_tokens), _lib.ptr(a_shared), a_shared.stride(0), _lib.ptr(ws),
+        _lib.ptr(c_shared), c_shared.stride(0), a_shared.shape[0], int(n_out), int(K), int(gated),
+        _lib.stream(),
+    )
+
+
 def smem_bytes(cfg: dict, fused: bool) -> int:
     """LDS bytes of the mapping this cfg selects (`moe_gateup.smem_bytes`'s question)."""
     bm = cfg["BLOCK_M"]

@@ -39,7 +39,7 @@ int glm52_add_rmsnorm(const void* x, const void* res, const void* w, void* h1, v
  *   stride_we == 1: the reference's [H, E] layout, read by the fp64 MFMA mapping; small T
  *     splits K and needs a workspace of glm52_router_workspace_bytes(T, H, E) bytes;
  *   stride_wk == 1: gate rows [E, H], one wave per expert row; no workspace.
- * E <= 256, E % 16 == 0, H % 32 == 0, H <= 8192; wgt 16-byte aligned. */
+ * E <= 256, E % 16 == 0, H % 64 == 0, H <= 8192; wgt 16-byte aligned. */
 int glm52_router_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
                         int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
                         void* workspace, int64_t workspace_bytes, int T, int H, int E,
@@ -81,6 +81,24 @@ int glm52_router_topk_align(const float* logits, int64_t stride_l, const float* 
                             int32_t* sorted_token_ids, int32_t* expert_ids,
                             int32_t* num_tokens_post_padded, hipStream_t stream);
 
+/* Decode front end in one launch (T <= 4): ResAdd + RMSNorm (h1, y), router logits from
+ * the gate rows ([E, H], K contiguous), sigmoid + biased top-k, renormalisation and
+ * scaling, and the dispatch layout; outputs bit-identical to glm52_add_rmsnorm +
+ * glm52_router_logits + glm52_router_topk_align.  Replaces the chain
+ * add_rmsnorm.fused_add_rmsnorm (glm52/kernels/add_rmsnorm.py:234-236) ->
+ * norm_router.router_gemm -> topk_only (glm52/kernels/norm_router.py:347-354) ->
+ * reference.moe_align_block_size (glm52/reference.py:85-128).  `counter` is one int32
+ * that must be zero before the first launch; the kernel leaves it zero.  Launches that
+ * overlap on one counter race. */
+int glm52_decode_front(const void* x, int64_t stride_x, const void* res, int64_t stride_r,
+                       const void* w_norm, void* h1, int64_t stride_h, void* y, int64_t stride_y,
+                       const void* gate, int64_t stride_g, const float* bias, float* logits,
+                       int64_t stride_l, float* topw, int64_t stride_w, int32_t* topi,
+                       int64_t stride_i, int T, int H, int E, int topk, float eps, float scale,
+                       int norm_prob, int block_m, int capacity, int32_t* sorted_token_ids,
+                       int32_t* expert_ids, int32_t* num_tokens_post_padded, int32_t* counter,
+                       hipStream_t stream);
+
 /* Grouped expert GEMM on bf16 MFMA.  Replaces moe_gateup.launch_gateup
  * (glm52/kernels/moe_gateup.py:199-248; gated = fused SwiGLU, gate_up_offset = I) and
  * moe_down_merge.launch_down with fuse_merge=False (glm52/kernels/moe_down_merge.py:427-476;
@@ -95,6 +113,20 @@ int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* 
                    const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
                    int capacity, int block_m, int num_valid_tokens, int n_out, int k, int gated,
                    int variant, hipStream_t stream);
+
+/* glm52_moe_gemm (weight-streaming mapping, block_m = 16) with the shared expert in the
+ * same launch: an extra expert with weights w_shared ([N, K], K contiguous, rows strided
+ * like w) applied to rows 0 .. shared_rows - 1 of a_shared, without routing weight,
+ * written to c_shared.  Replaces the routed + shared launch pairs of the reference chain
+ * (launch_gateup twice, launch_down twice: glm52/bench/bench_layer.py:430-480). */
+int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row_div, const void* w,
+                          int64_t stride_we, int64_t stride_wn, int gate_up_offset, void* c,
+                          int64_t stride_cm, const float* topk_weights,
+                          const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                          const int32_t* num_tokens_post_padded, int capacity, int block_m,
+                          int num_valid_tokens, const void* a_shared, int64_t stride_as,
+                          const void* w_shared, void* c_shared, int64_t stride_cs,
+                          int shared_rows, int n_out, int k, int gated, hipStream_t stream);
 
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */

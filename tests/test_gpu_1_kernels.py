@@ -12,7 +12,8 @@ import pytest
 import torch
 
 from fusion_amd import _lib
-from fusion_amd.dispatch import capacity, moe_align_block_size, topk_align_into
+from fusion_amd.dispatch import (capacity, decode_front_into, moe_align_block_size,
+                                 topk_align_into)
 from fusion_amd.kernels import add_rmsnorm as KN
 from fusion_amd.kernels import merge_resadd as KM
 from fusion_amd.kernels import moe_down_merge as KD
@@ -88,8 +89,9 @@ def test_add_rmsnorm_strided_rows(gpu):
 
 
 # ------------------------------------------------------------------ router
-@pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (13, "zipf"), (32, "normal"),
-                                    (100, "zero"), (2048, "normal"), (2048, "zipf")])
+@pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (8, "zipf"), (13, "zipf"),
+                                    (32, "normal"), (100, "zero"), (2048, "normal"),
+                                    (2048, "zipf")])
 def test_router_bitwise(gpu, T, bias):
     say(f"router T={T} bias={bias}")
     fe = front_end(T, bias=bias)
@@ -148,6 +150,63 @@ def test_router_golden_config0(gpu):
                               {"correction_bias": fe.bias.to(gpu)})
     assert np.array_equal(topi.cpu().numpy(), g["topk_ids"])
     np.testing.assert_allclose(topw.cpu().numpy(), g["topk_weights"], rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+@pytest.mark.parametrize("bias", ["normal", "zipf", "zero"])
+def test_decode_front_bitwise(gpu, T, bias):
+    """The one-launch decode front end against the oracle's exact rule, on three
+    launches in a row (the arrival counter must come back to zero after each)."""
+    say(f"decode front T={T} bias={bias}")
+    fe = front_end(T, bias=bias)
+    x, r, w = fe.x.to(gpu), fe.r.to(gpu), fe.w_norm.to(gpu)
+    gate_rows = fe.gate.to(gpu).contiguous()
+    b = None if bias == "zero" else fe.bias.to(gpu)
+    cfg = {"correction_bias": b}
+    y_o, h_o = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    lg_o, w_o, ids_o = O.router_exact(y_o, fe.wgt, None if b is None else fe.bias.numpy())
+    bm = 16
+    rs, re_, rn = O.moe_align_block_size(ids_o, bm, 256)
+    n = int(rn[0])
+    cap = capacity(T * 8, bm, 256)
+    counter = torch.zeros(1, dtype=torch.int32, device=gpu)
+    for rep in range(3):
+        h, y = torch.full_like(x, float("nan")), torch.full_like(x, float("nan"))
+        logits = torch.full((T, 256), float("nan"), device=gpu)
+        topw = torch.empty(T, 8, dtype=torch.float32, device=gpu)
+        topi = torch.empty(T, 8, dtype=torch.int32, device=gpu)
+        sti = torch.empty(cap, dtype=torch.int32, device=gpu)
+        eids = torch.empty(cap // bm, dtype=torch.int32, device=gpu)
+        ntp = torch.empty(1, dtype=torch.int32, device=gpu)
+        decode_front_into(x, r, w, h, y, gate_rows, cfg, logits, topw, topi, bm, sti, eids, ntp,
+                          counter)
+        torch.cuda.synchronize()
+        assert int(counter.item()) == 0, "arrival counter not reset"
+        assert np.array_equal(u16(h), u16(h_o)) and np.array_equal(u16(y), u16(y_o))
+        assert np.array_equal(logits.cpu().numpy(), lg_o)
+        assert np.array_equal(topi.cpu().numpy(), ids_o)
+        assert np.array_equal(topw.cpu().numpy(), w_o)
+        assert int(ntp.item()) == n
+        assert np.array_equal(sti.cpu().numpy()[:n], rs)
+        assert np.array_equal(eids.cpu().numpy()[: n // bm], re_)
+        assert (sti.cpu().numpy()[n:] == T * 8).all() and (eids.cpu().numpy()[n // bm:] == -1).all()
+
+
+def test_decode_front_rejects_large_T(gpu):
+    T = 5
+    fe = front_end(T)
+    x = fe.x.to(gpu)
+    gate_rows = fe.gate.to(gpu).contiguous()
+    cap = capacity(T * 8, 16, 256)
+    bufs = [torch.empty(cap, dtype=torch.int32, device=gpu),
+            torch.empty(cap // 16, dtype=torch.int32, device=gpu),
+            torch.empty(1, dtype=torch.int32, device=gpu)]
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        decode_front_into(x, x, fe.w_norm.to(gpu), x.clone(), x.clone(), gate_rows,
+                          {"correction_bias": fe.bias.to(gpu)},
+                          torch.empty(T, 256, device=gpu), torch.empty(T, 8, device=gpu),
+                          torch.empty(T, 8, dtype=torch.int32, device=gpu), 16, *bufs,
+                          torch.zeros(1, dtype=torch.int32, device=gpu))
 
 
 # ------------------------------------------------------------------ dispatch layout
@@ -277,6 +336,41 @@ def test_grouped_gemm_full_width(gpu):
         twf = tw.reshape(-1).contiguous()
         KD.launch_down(act, w2g, y, twf.to(gpu), sti, eids, ntp, T * k, k, cfg, False)
         _close(y, _down_ref(act, w2, ids, tw), f"w2 {variant}")
+
+
+@pytest.mark.parametrize("T", [1, 3, 16])
+def test_moe_gemm_shared_matches_separate_launches(gpu, T):
+    """Routed + shared expert in one weight-streaming launch: the same bits as the two
+    separate launches (routed layout, and the shared expert's one-expert layout)."""
+    from fusion_amd.block import shared_layout
+
+    say(f"moe_gemm_shared T={T}")
+    E, H, I, k = 16, 6144, 2048, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 40 + T, gpu)
+    g = torch.Generator().manual_seed(77)
+    w13s = (torch.randn(1, 2 * I, H, generator=g) * 0.05).to(BF16).to(gpu)
+    w2s = (torch.randn(1, H, I, generator=g) * 0.05).to(BF16).to(gpu)
+    ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
+    twf = tw.reshape(-1).contiguous().to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), 16, E)
+    ssti, seids, sntp = shared_layout(T, 16, gpu)
+    cfg = {"BLOCK_M": 16}
+    R = T * k
+    act, act_s = torch.empty(R, I, dtype=BF16, device=gpu), torch.empty(T, I, dtype=BF16, device=gpu)
+    KG.moe_gemm(ag, k, w13g, act, None, sti, eids, ntp, R, I, I, True, cfg)
+    KG.moe_gemm(ag, 1, w13s, act_s, None, ssti, seids, sntp, T, I, I, True, cfg)
+    y, s_out = torch.empty(R, H, dtype=BF16, device=gpu), torch.empty(T, H, dtype=BF16, device=gpu)
+    KG.moe_gemm(act, 1, w2g, y, twf, sti, eids, ntp, R, H, 0, False, cfg)
+    KG.moe_gemm(act_s, 1, w2s, s_out, None, ssti, seids, sntp, T, H, 0, False, cfg)
+    act2, act_s2 = torch.full_like(act, float("nan")), torch.full_like(act_s, float("nan"))
+    KG.moe_gemm_shared(ag, k, w13g, act2, None, sti, eids, ntp, R, I, I, True, cfg, ag, w13s,
+                       act_s2)
+    y2, s_out2 = torch.full_like(y, float("nan")), torch.full_like(s_out, float("nan"))
+    KG.moe_gemm_shared(act2, 1, w2g, y2, twf, sti, eids, ntp, R, H, 0, False, cfg, act_s2, w2s,
+                       s_out2)
+    torch.cuda.synchronize()
+    assert torch.equal(act2, act) and torch.equal(act_s2, act_s)
+    assert torch.equal(y2, y) and torch.equal(s_out2, s_out)
 
 
 def test_layout_mismatch_is_rejected(gpu):
