@@ -20,10 +20,8 @@
 // Two mappings, picked by the gate's layout.  Rows ([E, H], K contiguous, used at small
 // T): a wave per expert streams its row once (`router_rows_kernel`).  Columns ([H, E],
 // the reference kernel's layout): the logits run on the fp64 matrix cores
-// (`v_mfma_f64_16x16x4_f64`): a workgroup owns 16
-// tokens x all experts, each of its four waves 64 experts (four 16 x 16 fp64 tiles), and
-// walks a K slice through two LDS buffers holding y (as fp64) and the gate weight (as
-// stored), the next chunk's loads in flight while the current chunk is multiplied.  Small T
+// (`v_mfma_f64_16x16x4_f64`), a workgroup per 32 tokens x all experts of a K slice, gate
+// and token chunks staged through two LDS buffers (`router_logits_kernel`).  Small T
 // splits K over KS workgroups; their fp64 partials land in a caller-provided workspace
 // and are summed in a fixed order (by `router_reduce_kernel`, or inside the top-k kernel)
 // before the single rounding to fp32.
@@ -41,119 +39,147 @@ typedef double doublex4_t __attribute__((ext_vector_type(4)));
 
 namespace {
 
-constexpr int KC = 64;    // k granularity of the [H, E] mapping (its largest chunk)
-constexpr int TB = 16;    // tokens per workgroup (one fp64 MFMA tile)
+constexpr int KC = 64;    // K split granularity: every split slice is a multiple of it
+constexpr int TB = 32;    // tokens per workgroup of the [H, E] mapping
 constexpr int EMAX = kMaxE;
 
 GLM52_DEV doublex4_t mfma64(double a, double b, doublex4_t c) {
   return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
 }
 
-// grid = (ceil(T / 16), KS); block = 256.  KS == 1: fp32 logits out; else fp64 partials.
-// K advances in chunks of KC (64 for a bf16 gate, 32 for fp32) through two LDS buffers:
-// the next chunk's gate rows and token rows are loaded into registers (16-byte loads)
-// while the MFMAs consume the current chunk, then stored to the other buffer.
+// Bank spread of the gate rows in LDS: expert column c's slot in a row holds two halves
+// (experts c*16 .. +7 and c*16+8 .. +15); half h is stored at position h ^ gsw(c), so the 16
+// lanes of one operand read cover distinct bank groups.
+GLM52_DEV int gsw(int c) { return ((c >> 2) ^ (c >> 3)) & 1; }
+
+// [H, E] mapping on `v_mfma_f64_16x16x4f64`.  grid = (ceil(T / 32), KS); block = 256.
+// A workgroup owns 32 tokens x all (<= 256) experts of one K slice; wave (th, eh) owns
+// tokens th*16 .. +15 and the experts c*16 + eh*8 + j (c < 16 the MFMA column, j < 8 its
+// tile), so a lane's 8 B operands of one MFMA step are 8 adjacent gate entries (one
+// 16-byte LDS read).  K is walked in chunks of KCH through two LDS buffers; inside a
+// chunk, lane group g of an MFMA takes k = g * KCH/4 + s at step s (the sum is order-
+// free, the same k feeds both operands), so a lane's token operands of the whole chunk
+// are KCH/4 adjacent y entries.  The next chunk is loaded into registers while the
+// current one is multiplied.  Results are staged through LDS for coalesced stores: fp32
+// logits when KS == 1, else fp64 partials part[ks, t, e].
 template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swg,
     float* __restrict__ logits, int64_t sl, double* __restrict__ part, int T, int H, int E) {
   using WT = typename std::conditional<WG_F32, float, uint16_t>::type;
-  constexpr int KCH = WG_F32 ? 32 : 64;     // k rows per chunk
-  constexpr int VEC = WG_F32 ? 4 : 8;       // gate elements per 16-byte vector
-  constexpr int GV = KCH * EMAX / VEC / 256;  // gate vectors per thread per chunk
-  constexpr int YV = TB * KCH / 8;          // 16-byte y vectors per chunk (threads 0 .. YV-1)
-  static_assert(YV <= 256 && GV >= 1, "chunk");
-  __shared__ double ys[2][TB][KCH + 1];
-  __shared__ __attribute__((aligned(16))) WT ws[2][KCH][EMAX + (WG_F32 ? 4 : 8)];
+  constexpr int EPV = 16 / sizeof(WT);        // gate entries per 16-byte vector
+  constexpr int CPR = EMAX / EPV;              // 16-byte vectors per gate row (32 or 64)
+  constexpr int KCH = 2048 / CPR;              // k per chunk (64 bf16, 32 fp32): 32 KB / 64 KB
+  constexpr int SPG = KCH / 4;                 // MFMA steps per chunk
+  constexpr int YC = KCH / 8;                  // 16-byte y vectors per token row and chunk
+  constexpr int YLD = KCH + 8;                 // y row pitch in LDS (bf16)
+  constexpr int GSZ = KCH * EMAX * sizeof(WT); // bytes of one gate chunk: 32 KB
+  static_assert(2 * GSZ >= TB * EMAX * 8, "the epilogue stage fits in the gate buffers");
+  __shared__ __attribute__((aligned(16))) WT gs[2][KCH * EMAX];
+  __shared__ __attribute__((aligned(16))) uint16_t ys[2][TB * YLD];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wv = tid / kWave;
+  const int c = lane % 16, g = lane / 16;
+  const int th = wv & 1, eh = wv >> 1;
   const int t0 = blockIdx.x * TB;
   const int KS = gridDim.y;
   const int ksl = H / KS;
   const int kbeg = blockIdx.y * ksl;
   const int nch = ksl / KCH;
   const WT* wg = static_cast<const WT*>(wg_raw);
-  const int ntile = E / 16;
-  const int vpr = E / VEC;  // gate vectors per k row
 
-  uint4 rg[GV], ry;
-  auto gload = [&](int c) {
-    const int k0 = kbeg + c * KCH;
+  // LDS element offset, inside a gate row, of 16-byte vector m (entries m*EPV .. +EPV-1)
+  auto gpos = [](int m) {
+    const int per_col = 16 / EPV;  // vectors per expert column (2 bf16, 4 fp32)
+    const int cc = m / per_col, w = m % per_col;
+    const int half = w / (per_col / 2), q = w % (per_col / 2);
+    return (cc * per_col + ((half ^ gsw(cc)) * (per_col / 2)) + q) * EPV;
+  };
+
+  uint4 rg[8], ry = make_uint4(0, 0, 0, 0);
+  auto gload = [&](int ch) {
+    const int k0 = kbeg + ch * KCH;
 #pragma unroll
-    for (int i = 0; i < GV; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const int q = tid + i * 256;
-      const int kk = q / (EMAX / VEC), v = q % (EMAX / VEC);
-      rg[i] = v < vpr ? *reinterpret_cast<const uint4*>(wg + (int64_t)(k0 + kk) * swg + v * VEC)
-                      : make_uint4(0, 0, 0, 0);
+      const int kk = q / CPR, m = q % CPR;
+      rg[i] = m * EPV < E ? *reinterpret_cast<const uint4*>(wg + (int64_t)(k0 + kk) * swg + m * EPV)
+                          : make_uint4(0, 0, 0, 0);
     }
-    if (tid < YV) {
-      const int t = tid / (KCH / 8), kc = tid % (KCH / 8);
+    if (tid < TB * YC) {
+      const int t = tid / YC, kc = tid % YC;
       ry = t0 + t < T ? *reinterpret_cast<const uint4*>(y + (int64_t)(t0 + t) * sy + k0 + kc * 8)
                       : make_uint4(0, 0, 0, 0);
     }
   };
   auto sstore = [&](int b) {
 #pragma unroll
-    for (int i = 0; i < GV; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const int q = tid + i * 256;
-      const int kk = q / (EMAX / VEC), v = q % (EMAX / VEC);
-      *reinterpret_cast<uint4*>(&ws[b][kk][v * VEC]) = rg[i];
+      const int kk = q / CPR, m = q % CPR;
+      *reinterpret_cast<uint4*>(&gs[b][kk * EMAX + gpos(m)]) = rg[i];
     }
-    if (tid < YV) {
-      const int t = tid / (KCH / 8), kc = tid % (KCH / 8);
-      float f[8];
-      unpack8(ry, f);
-#pragma unroll
-      for (int q = 0; q < 8; ++q) ys[b][t][kc * 8 + q] = (double)f[q];
+    if (tid < TB * YC) {
+      const int t = tid / YC, kc = tid % YC;
+      *reinterpret_cast<uint4*>(&ys[b][t * YLD + kc * 8]) = ry;
     }
   };
 
-  doublex4_t acc[4];
+  doublex4_t acc[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = doublex4_t{0.0, 0.0, 0.0, 0.0};
+  for (int j = 0; j < 8; ++j) acc[j] = doublex4_t{0.0, 0.0, 0.0, 0.0};
+  // the lane's 8 gate entries of a row: experts c*16 + eh*8 .. +7
+  const int boff = gpos((c * 16 + eh * 8) / EPV);
 
   gload(0);
   sstore(0);
   __syncthreads();
-  for (int c = 0; c < nch; ++c) {
-    const int cur = c & 1;
-    if (c + 1 < nch) gload(c + 1);
+  for (int ch = 0; ch < nch; ++ch) {
+    const int cur = ch & 1;
+    if (ch + 1 < nch) gload(ch + 1);
+    float af[SPG];
+    {
+      const uint16_t* yr = &ys[cur][(th * 16 + c) * YLD + g * SPG];
 #pragma unroll
-    for (int k4 = 0; k4 < KCH; k4 += 4) {
-      const double a = ys[cur][lane % 16][k4 + lane / 16];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tile = wv * 4 + j;
-        if (tile < ntile) {
-          const WT raw = ws[cur][k4 + lane / 16][tile * 16 + lane % 16];
-          double b;
-          if constexpr (WG_F32) b = (double)raw;
-          else b = (double)bf16_to_f32(raw);
-          acc[j] = mfma64(a, b, acc[j]);
-        }
-      }
+      for (int v = 0; v < SPG / 8; ++v) unpack8(*reinterpret_cast<const uint4*>(yr + v * 8), af + v * 8);
     }
-    if (c + 1 < nch) sstore(cur ^ 1);
+    const WT* gb = &gs[cur][(g * SPG) * EMAX + boff];
+#pragma unroll
+    for (int s = 0; s < SPG; ++s) {
+      float wf[8];
+      if constexpr (WG_F32) {
+        const float4 w0 = *reinterpret_cast<const float4*>(gb + s * EMAX);
+        const float4 w1 = *reinterpret_cast<const float4*>(gb + s * EMAX + 4);
+        wf[0] = w0.x; wf[1] = w0.y; wf[2] = w0.z; wf[3] = w0.w;
+        wf[4] = w1.x; wf[5] = w1.y; wf[6] = w1.z; wf[7] = w1.w;
+      } else {
+        unpack8(*reinterpret_cast<const uint4*>(gb + s * EMAX), wf);
+      }
+      const double a = (double)af[s];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = mfma64(a, (double)wf[j], acc[j]);
+    }
+    if (ch + 1 < nch) sstore(cur ^ 1);
     __syncthreads();
   }
 
-  // the fp64 MFMA result layout: register v of lane l holds row (l / 16) + 4 v (token)
-  // and column l % 16 (expert) of the tile -- unlike the bf16 16x16x32 layout, where the
-  // row is 4 (l / 16) + v
+  // fp64 MFMA result layout: register v of lane (c, g) is row g + 4 v (token), column c
+  double* st = reinterpret_cast<double*>(&gs[0][0]);  // [TB][EMAX]
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tile = wv * 4 + j;
-    if (tile >= ntile) continue;
-    const int e = tile * 16 + lane % 16;
+  for (int v = 0; v < 4; ++v) {
+    const int tl = th * 16 + g + 4 * v;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int t = t0 + lane / 16 + 4 * v;
-      if (t >= T) continue;
-      if (KS == 1) logits[(int64_t)t * sl + e] = (float)acc[j][v];
-      else part[((int64_t)blockIdx.y * T + t) * E + e] = acc[j][v];
-    }
+    for (int j = 0; j < 8; ++j) st[tl * EMAX + c * 16 + eh * 8 + j] = acc[j][v];
+  }
+  __syncthreads();
+  const int nt = min(TB, T - t0);
+  for (int q = tid; q < nt * E; q += 256) {
+    const int tl = q / E, e = q % E;
+    const double s = st[tl * EMAX + e];
+    if (KS == 1) logits[(int64_t)(t0 + tl) * sl + e] = (float)s;
+    else part[((int64_t)blockIdx.y * T + t0 + tl) * E + e] = s;
   }
 }
 
@@ -290,7 +316,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 int choose_ks(int T, int H) {
   const int tblocks = (T + TB - 1) / TB;
   int ks = 1;
-  while (tblocks * ks < 128 && ks < 16 && (H % (KC * ks * 2)) == 0) ks *= 2;
+  while (tblocks * ks < 256 && ks < 32 && (H % (KC * ks * 2)) == 0) ks *= 2;
   return ks;
 }
 

@@ -28,7 +28,7 @@ def test_router_workspace_query():
 
     assert KR.workspace_bytes(1) > 0  # decode splits K
     assert KR.workspace_bytes(8192) == 0  # prefill covers the chip without a split
-    assert KR.workspace_bytes(256) == 8 * 256 * 256 * 8  # 16 token blocks x 8 K slices
+    assert KR.workspace_bytes(256) == 32 * 256 * 256 * 8  # 8 token blocks x 32 K slices
 
 
 def test_library_exports_every_declared_symbol():
