@@ -12,6 +12,15 @@ GLM52_DEV floatx4_t mfma16(const uint4& a, const uint4& b, floatx4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+// C(32 x 32, fp32) += A(32 x 16) . B(16 x 32) on bf16 MFMA.  Lane l supplies row l % 32 of A
+// and column l % 32 of B, each as the 8 consecutive k starting at 8 (l / 32); the result
+// register i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4, column l % 32.
+GLM52_DEV floatx16_t mfma32(const uint4& a, const uint4& b, floatx16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
@@ -68,5 +77,9 @@ struct GemmArgs {
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
 // returns GLM52_EUNSUPPORTED for a block size or shape it has no instance for.
 int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
+
+// The 512-row W tile mapping (moe_gemm_wide.hip): GLM52_EUNSUPPORTED for a block size or
+// shape it has no instance for.
+int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
 
 }  // namespace glm52

@@ -365,9 +365,10 @@ int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
 
 }  // namespace
 
-// variant: 0 = choose (stream when BM == 16, wide when BM is 64 or 128, tiled otherwise),
-// 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages
-// (moe_gemm_wide.hip; block_m in {64, 128}).
+// variant: 0 = choose (stream when BM == 16; 512-row W tiles when BM is 64 or 128, else the
+// 256-row wide mapping for shapes the 512-row one does not cover; tiled otherwise),
+// 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages, 5 = 512-row
+// W tiles (moe_gemm_wide.hip; block_m in {64, 128}).
 extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                               int64_t stride_we, int64_t stride_wn, int gate_up_offset,
                               void* c, int64_t stride_cm, const float* topk_weights,
@@ -391,6 +392,13 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
              nullptr, 0, nullptr, nullptr, 0, 0, a_bytes(num_valid_tokens, a_row_div, stride_am, k), 0};
   const bool weighted = topk_weights != nullptr;
   const bool auto_wide = variant == 0 && (block_m == 64 || block_m == 128);
+  if (variant == 5 || auto_wide) {
+    // the 512-row mapping addresses token rows with 32-bit byte offsets; shapes it has no
+    // instance for fall back to the 256-row mapping when the mapping was not forced
+    const int rc = g.a_bytes < 0x7ffffff0 ? launch_wide512(g, capacity, gated != 0, weighted, stream)
+                                          : GLM52_EUNSUPPORTED;
+    if (rc != GLM52_EUNSUPPORTED || variant == 5) return rc;
+  }
   if (variant == 3 || variant == 4 || auto_wide) {
     g.stage_k = variant == 4 ? 32 : 64;
     return launch_wide(g, capacity, gated != 0, weighted, stream);
@@ -448,12 +456,16 @@ extern "C" int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row
                   : launch_stream<false, false>(g, capacity, stream);
 }
 
-// Self-test of the MFMA result layouts this library assumes, for the bf16 16x16x32 and
-// the fp64 16x16x4 instructions: A[r][k] = r + 1 for the first 16 k, B = identity on
-// those k -> C[r][c] = r + 1.  Lane l supplies row / column l % 16 and k group l / 16;
-// the result's register i of lane l is row 4 (l / 16) + i for bf16 and (l / 16) + 4 i
-// for fp64, column l % 16 in both.  Writes two 16 x 16 fp32 matrices row-major to `out`
-// (512 floats): [0, 256) from the bf16 MFMA, [256, 512) from the fp64 MFMA.
+// Self-test of the MFMA result layouts this library assumes, for the bf16 16x16x32, the fp64
+// 16x16x4 and the bf16 32x32x16 instructions.  16x16 probes: A[r][k] = r + 1 for the first 16
+// k, B = identity on those k -> C[r][c] = r + 1.  Lane l supplies row / column l % 16 and k
+// group l / 16; the result's register i of lane l is row 4 (l / 16) + i for bf16 and
+// (l / 16) + 4 i for fp64, column l % 16 in both.  32x32 probe: A[r][0] = r, A[r][1] = 1,
+// B[0][c] = 32, B[1][c] = c, so C[r][c] = 32 r + c; lane l supplies row / column l % 32 and
+// the 8 k from 8 (l / 32); register i of lane l is row 8 (i / 4) + 4 (l / 32) + i % 4,
+// column l % 32.  Writes 1536 floats to `out`: [0, 256) and [256, 512) the two 16 x 16
+// matrices row-major (bf16, fp64 MFMA), [512, 1536) the raw 32x32 results, lane-major
+// (out[512 + 16 l + i] = register i of lane l).
 typedef double doublex4_t __attribute__((ext_vector_type(4)));
 namespace {
 __global__ void mfma_layout_probe(float* out) {
@@ -477,6 +489,19 @@ __global__ void mfma_layout_probe(float* out) {
   }
   // fp64 result layout: register i of lane (r, g) is row g + 4 i
   for (int i = 0; i < 4; ++i) out[256 + (g + 4 * i) * 16 + r] = (float)d[i];
+  // bf16 32x32x16
+  const int r32 = lane % 32, h = lane / 32;
+  float a32[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, b32[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (h == 0) {
+    a32[0] = (float)r32;
+    a32[1] = 1.f;
+    b32[0] = 32.f;
+    b32[1] = (float)r32;
+  }
+  floatx16_t c32;
+  for (int i = 0; i < 16; ++i) c32[i] = 0.f;
+  c32 = mfma32(pack8(a32), pack8(b32), c32);
+  for (int i = 0; i < 16; ++i) out[512 + lane * 16 + i] = c32[i];
 }
 }  // namespace
 

@@ -29,6 +29,8 @@
 // once and served to the others from the XCD's L2.
 #include "moe_gemm.h"
 
+#include <type_traits>
+
 using namespace glm52;
 
 namespace {
@@ -63,6 +65,15 @@ GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
                : "s"(lds_base), "v"(gptr)
+               : "memory");
+}
+
+// The same load with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset:
+// lane l's 16 bytes at base + voff land at byte `lds_base` + 16 l.
+GLM52_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_base), "v"(voff), "s"(sbase)
                : "memory");
 }
 
@@ -323,5 +334,267 @@ namespace glm52 {
 int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st) {
   if (gated) return weighted ? launch_bm<true, true>(a, capacity, st) : launch_bm<true, false>(a, capacity, st);
   return weighted ? launch_bm<false, true>(a, capacity, st) : launch_bm<false, false>(a, capacity, st);
+}
+}  // namespace glm52
+
+// ------------------------------------------------------------------------------------
+// 512-row W tiles on the 32x32x16 MFMA.  A workgroup owns MT tokens (one layout block) x 512
+// rows of W[e]; wave w computes the W rows w*128 .. +127 (gated: 64 `gate` rows and the
+// matching 64 `up` rows) against all MT tokens: a 128 x MT wave tile of 4 x MT/32 blocks of
+// 32 x 32, W as the first MFMA operand.  All four waves share the staged token rows.
+//
+// Pipeline.  K advances in 32-k stages through a ring of four LDS buffers filled by direct
+// global -> LDS loads.  While the MFMAs of stage kt run on fragments already in registers,
+// the same instruction stream reads the fragments of stage kt+1 from LDS and issues the
+// loads of stage kt+3; the three kinds are interleaved in a fixed order (scheduling
+// barriers pin it), so neither the LDS reads nor the load issue stall the matrix core.
+// Loads past the last stage re-read the last stage into the free buffer, so every stage
+// has the same shape and the waits are the same constant.  Staged row r keeps its 16-byte
+// chunk c at c ^ ((r >> 2) & 3): the 16 lanes served together read 16 distinct bank groups.
+//
+// Output.  Inside each 32-row group of the W tile, LDS row p holds W row
+// ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); a lane's 16 results of a 32 x 32 block are
+// then 16 consecutive outputs of one token, written with two 16-byte stores.  A gated tile
+// pairs `gate` row n and `up` row n in the same lane and register, so SwiGLU runs in
+// registers.
+// ------------------------------------------------------------------------------------
+namespace {
+
+// W row (inside its 32-row group) held at LDS row p.
+GLM52_DEV int phi32(int p) { return ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); }
+
+template <int MT, bool GATED, bool WEIGHTED>
+__global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
+  constexpr int NTW = 512;         // W rows per tile
+  constexpr int BKS = 32;          // k per stage
+  constexpr int NSTAGE = 4;
+  constexpr int RPI = 16;          // staged rows per load instruction (64 lanes x 16 B / 64 B)
+  constexpr int TF = MT / 32;      // token blocks of 32
+  constexpr int NO = GATED ? NTW / 2 : NTW;
+  constexpr int WI = NTW / RPI / 4;  // W load instructions per wave and stage (8)
+  constexpr int AI = MT / RPI / 4;   // token-row load instructions per wave and stage
+  constexpr int IPS = WI + AI;
+  constexpr int SROWS = NTW + MT;
+  constexpr int SELEM = SROWS * BKS;  // elements per stage
+  static_assert(AI >= 1 && TF >= 1 && IPS < 64, "stage shape");
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  const int wvu = __builtin_amdgcn_readfirstlane(wv);
+  const int l32 = lane % 32, h = lane / 32;
+
+  const int ntp = *p.ntp;
+  const int num_m = ntp / MT;
+  const int num_n = p.n_out / NO;
+  const int items = num_m * num_n;
+  const int nk = p.K / BKS;
+  const int per_xcd = (items + 7) / 8;
+  const int span = per_xcd * 8;
+
+  // fragment reads: lane (l32, h) reads logical chunk 2 ks + h of row base + l32 (base % 32 == 0)
+  const int rd0 = l32 * BKS + (((0 + h) ^ ((l32 >> 2) & 3)) * 8);
+  const int rd1 = l32 * BKS + (((2 + h) ^ ((l32 >> 2) & 3)) * 8);
+  // load slots: lane -> row lane / 4 of the instruction's 16-row slab, physical chunk lane % 4
+  const int dr = lane >> 2;
+  const int dc = (lane & 3) ^ ((dr >> 2) & 3);  // the logical chunk that lands in that slot
+  const uint32_t ring_base = lds_addr(ring);
+
+  for (int it = blockIdx.x; it < span; it += gridDim.x) {
+    const int L = (it % 8) * per_xcd + it / 8;
+    if (L >= items) continue;
+    // expert-aligned order (as moe_gemm_dma_kernel): column tile major, row block fastest
+    const int b = L / num_n;
+    const int eb = p.eids[b];
+    int mb = b, me = b + 1;
+    while (mb > 0 && p.eids[mb - 1] == eb) --mb;
+    while (me < num_m && p.eids[me] == eb) ++me;
+    const int cnt = me - mb;
+    const int local = L - mb * num_n;
+    const int pid_n = local / cnt;
+    const int pid_m = mb + local % cnt;
+    const int row0 = pid_m * MT;
+    if (p.sti[row0] >= p.num_valid) continue;
+    const int e = p.eids[pid_m];
+    const int n0 = pid_n * NO;
+
+    // real tokens fill a prefix of the block: every wave counts them (no LDS, no barrier)
+    int nv_rows = 0;
+#pragma unroll
+    for (int q = 0; q < MT; q += kWave)
+      nv_rows += __popcll(__ballot(q + lane < MT && p.sti[row0 + q + lane] < p.num_valid));
+    nv_rows = __builtin_amdgcn_readfirstlane(nv_rows);
+    const int nvf = __builtin_amdgcn_readfirstlane(min(TF, (nv_rows + 31) / 32));
+
+    // W load instruction i of the wave fills slab rows i*16 .. +15: W rows
+    // wrow(i) + phi32(lane / 4) (wrow(i) wave-uniform), 16 bytes at logical chunk dc each;
+    // the lane's byte offsets inside W[e] (< 2^32: an expert's W is far smaller)
+    const uint16_t* wexp = p.W + (int64_t)e * p.swe;
+    uint32_t wvoff[WI];
+#pragma unroll
+    for (int i = 0; i < WI; ++i) {
+      const int f = i >> 1;
+      const int base = GATED ? (f >= 2 ? p.gu_off : 0) + n0 + wv * 64 + (f & 1) * 32
+                             : n0 + wv * 128 + f * 32;
+      wvoff[i] = (uint32_t)(((int64_t)(base + (i & 1) * 8 + phi32(dr)) * p.swn + dc * 8) * 2);
+    }
+    uint32_t avoff[AI];  // byte offsets of the lane's token rows in A (< 2^31, checked)
+#pragma unroll
+    for (int i = 0; i < AI; ++i) {
+      const int rl = wv * (MT / 4) + i * RPI + dr;
+      avoff[i] = (uint32_t)((p.sti[row0 + (rl < nv_rows ? rl : 0)] / p.a_div) * (int)p.sam + dc * 8) * 2u;
+    }
+
+    // the previous item's output stores and loads are done before this item's are counted
+    GLM52_WAIT_VMCNT(0);
+    auto issue_one = [&](int i, int kt) {  // load instruction i of stage kt (clamped)
+      const int kc = min(kt, nk - 1) * BKS;
+      const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
+      if (i < WI) {
+        dma16s(wexp + kc, wvoff[i], sb + (uint32_t)((wvu * 128 + i * RPI) * BKS * 2));
+      } else {
+        const int j = i - WI;
+        dma16s(p.A + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
+      }
+    };
+
+    auto run = [&](auto nv_tag) {
+      constexpr int NV = decltype(nv_tag)::value;
+      constexpr int NMF = 8 * NV;           // MFMAs per stage
+      constexpr int NRD = 8 + 2 * NV;       // fragment reads per stage
+      constexpr int NOPS = NRD + IPS;       // reads and loads spread over the MFMAs
+      floatx16_t acc[4][NV];
+#pragma unroll
+      for (int f = 0; f < 4; ++f)
+#pragma unroll
+        for (int t = 0; t < NV; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[f][t][i] = 0.f;
+      // fragments of two stages: [parity][k step][block]
+      uint4 fw[2][2][4], fa[2][2][NV];
+
+      auto read_op = [&](int q, const uint16_t* sb, uint4 (&dw)[2][4], uint4 (&da)[2][NV]) {
+        if (q < 8) {
+          const int ks = q / 4, f = q % 4;
+          dw[ks][f] = *reinterpret_cast<const uint4*>(sb + (wv * 128 + f * 32) * BKS + (ks ? rd1 : rd0));
+        } else {
+          const int ks = (q - 8) / NV, t = (q - 8) % NV;
+          da[ks][t] = *reinterpret_cast<const uint4*>(sb + (NTW + t * 32) * BKS + (ks ? rd1 : rd0));
+        }
+      };
+
+      // one stage: the MFMAs of stage kt on fragments [P], interleaved with the reads of
+      // stage kt+1 into fragments [1-P] and the loads of stage kt+3
+      auto stage = [&](int kt, auto par_tag) {
+        constexpr int P = decltype(par_tag)::value;
+        // stage kt+1 landed for this wave (stage kt+2 may still be in flight) and for
+        // every wave; every wave is done with the buffer refilled in this stage
+        GLM52_WAIT_VMCNT(IPS);
+        __syncthreads();
+        const uint16_t* sbn = ring + ((kt + 1) % NSTAGE) * SELEM;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int m = 0; m < NMF; ++m) {
+          const int ks = m / (4 * NV), f = (m / NV) % 4, t = m % NV;
+          acc[f][t] = mfma32(fw[P][ks][f], fa[P][ks][t], acc[f][t]);
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int o = 0; o < NOPS; ++o) {
+            if ((o * NMF) / NOPS == m) {  // op o goes after MFMA m
+              // alternate loads and reads while both remain
+              constexpr int both = 2 * (IPS < NRD ? IPS : NRD);
+              const bool is_load = o < both ? (o % 2) == 0 : IPS > NRD;
+              const int idx = o < both ? o / 2 : both / 2 + (o - both);
+              if (is_load) issue_one(idx, kt + NSTAGE - 1);
+              else read_op(idx, sbn, fw[1 - P], fa[1 - P]);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+      };
+
+      // prologue: stages 0 .. 2 in flight; stage 0 landed everywhere; its fragments read
+#pragma unroll
+      for (int st = 0; st < NSTAGE - 1; ++st)
+#pragma unroll
+        for (int i = 0; i < IPS; ++i) issue_one(i, st);
+      GLM52_WAIT_VMCNT(2 * IPS);
+      __syncthreads();
+#pragma unroll
+      for (int q = 0; q < NRD; ++q) read_op(q, ring, fw[0], fa[0]);
+
+#pragma unroll 1
+      for (int kt = 0; kt < nk; kt += 2) {  // nk is even (the launcher checks K % 64)
+        stage(kt, std::integral_constant<int, 0>{});
+        stage(kt + 1, std::integral_constant<int, 1>{});
+      }
+
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {
+        const int tok = p.sti[row0 + t * 32 + l32];
+        if (tok >= p.num_valid) continue;
+        uint16_t* crow = p.C + (int64_t)tok * p.scm;
+        if (GATED) {
+#pragma unroll
+          for (int fp = 0; fp < 2; ++fp) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = silu_mul(acc[fp][t][i], acc[fp + 2][t][i]);
+            uint16_t* dst = crow + n0 + wv * 64 + fp * 32 + h * 16;
+            *reinterpret_cast<uint4*>(dst) = pack8(v);
+            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+          }
+        } else {
+          float wgt = 1.f;
+          if (WEIGHTED) wgt = p.topw[tok];
+#pragma unroll
+          for (int f = 0; f < 4; ++f) {
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
+            uint16_t* dst = crow + n0 + wv * 128 + f * 32 + h * 16;
+            *reinterpret_cast<uint4*>(dst) = pack8(v);
+            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+          }
+        }
+      }
+    };
+    switch (nvf) {
+      case 1: run(std::integral_constant<int, 1>{}); break;
+      case 2: run(std::integral_constant<int, (TF >= 2 ? 2 : 1)>{}); break;
+      case 3: run(std::integral_constant<int, (TF >= 3 ? 3 : 1)>{}); break;
+      default: run(std::integral_constant<int, (TF >= 4 ? 4 : 1)>{}); break;
+    }
+    __syncthreads();  // the ring is refilled by the next item
+  }
+}
+
+template <int MT, bool GATED, bool WEIGHTED>
+int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
+  constexpr int NO = GATED ? 256 : 512;
+  if ((a.n_out % NO) || (a.K % 64)) return GLM52_EUNSUPPORTED;
+  const int items_max = (capacity / MT) * (a.n_out / NO);
+  int grid = items_max < 256 ? items_max : 256;
+  grid = ((grid + 7) / 8) * 8;
+  moe_gemm_w512_kernel<MT, GATED, WEIGHTED><<<grid, 256, 0, st>>>(a);
+  GLM52_RETURN_LAUNCH();
+}
+
+template <bool GATED, bool WEIGHTED>
+int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
+  switch (a.BM) {
+    case 64: return launch_w512<64, GATED, WEIGHTED>(a, capacity, st);
+    case 128: return launch_w512<128, GATED, WEIGHTED>(a, capacity, st);
+    default: return GLM52_EUNSUPPORTED;
+  }
+}
+
+}  // namespace
+
+namespace glm52 {
+int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st) {
+  if (gated) return weighted ? launch_w512_bm<true, true>(a, capacity, st) : launch_w512_bm<true, false>(a, capacity, st);
+  return weighted ? launch_w512_bm<false, true>(a, capacity, st) : launch_w512_bm<false, false>(a, capacity, st);
 }
 }  // namespace glm52

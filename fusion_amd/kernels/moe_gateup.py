@@ -12,9 +12,10 @@ conventions (`glm52/kernels/REFERENCES.md:41-51`): A rows are gathered with
 
 `cfg["BLOCK_M"]` must equal the layout's block size (checked).  `cfg["variant"]` may
 force "stream" (weight-streaming decode mapping), "tiled" (register-staged LDS tiles),
-"wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages) or
-"wide32" (the same with 32-k stages); by default BM = 16 streams, BM in {64, 128} runs
-"wide" and BM = 32 "tiled".
+"wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages), "wide32"
+(the same with 32-k stages) or "w512" (512-row W tiles on the 32x32x16 MFMA, 32-k stages);
+by default BM = 16 streams, BM in {64, 128} runs "w512" (falling back to "wide" for
+shapes it does not cover) and BM = 32 "tiled".
 """
 
 from __future__ import annotations
@@ -23,7 +24,7 @@ import torch
 
 from .. import _lib
 
-VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4}
+VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4, "w512": 5}
 
 
 def check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m: int) -> int:
@@ -103,7 +104,9 @@ def smem_bytes(cfg: dict, fused: bool) -> int:
     variant = cfg.get("variant")
     if variant == "stream" or (variant is None and bm == 16):
         return 8192
-    if variant in ("wide", "wide32") or (variant is None and bm in (64, 128)):
+    if variant == "w512" or (variant is None and bm in (64, 128)):
+        return 4 * (512 + bm) * 32 * 2
+    if variant in ("wide", "wide32"):
         stages, bk = (4, 32) if variant == "wide32" else (3, 64)
         return stages * (256 + bm) * bk * 2 + 4 * bm
     nb = 128

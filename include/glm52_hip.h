@@ -164,8 +164,9 @@ int glm52_block_merge(const void* y, int64_t stride_yt, int64_t stride_yk, const
 int glm52_stream_read(const void* buf, int64_t bytes, int nontemporal, int grid, uint32_t* sink,
                       hipStream_t stream);
 
-/* Self-test of the MFMA result layouts the kernels assume (bf16 16x16x32 and fp64
- * 16x16x4): writes two 16 x 16 fp32 matrices (512 floats) whose row r is all (r + 1).
+/* Self-test of the MFMA result layouts the kernels assume (bf16 16x16x32, fp64 16x16x4 and
+ * bf16 32x32x16): writes 1536 floats -- two 16 x 16 fp32 matrices whose row r is all (r + 1),
+ * then the 64 x 16 raw 32x32x16 results (lane-major) of C[r][c] = 32 r + c.
  * No counterpart in the reference. */
 int glm52_selftest_mfma_layout(float* out, hipStream_t stream);
 

@@ -37,12 +37,19 @@ def say(*a):
 
 # ------------------------------------------------------------------ MFMA layout
 def test_mfma_layout_selftest(gpu):
-    out = torch.zeros(512, dtype=torch.float32, device=gpu)
+    out = torch.zeros(1536, dtype=torch.float32, device=gpu)
     _lib.call("glm52_selftest_mfma_layout", _lib.ptr(out), _lib.stream())
-    m = out.view(2, 16, 16).cpu()
+    m = out[:512].view(2, 16, 16).cpu()
     want = torch.arange(1, 17, dtype=torch.float32).unsqueeze(1).expand(16, 16)
     assert torch.equal(m[0], want), m[0]
     assert torch.equal(m[1], want), m[1]
+    # 32x32x16: register i of lane l holds C[8 (i / 4) + 4 (l / 32) + i % 4][l % 32] = 32 row + col
+    got = out[512:].view(64, 16).cpu()
+    lane = torch.arange(64).unsqueeze(1)
+    i = torch.arange(16).unsqueeze(0)
+    row = 8 * (i // 4) + 4 * (lane // 32) + i % 4
+    col = (lane % 32).expand(64, 16)
+    assert torch.equal(got, (32 * row + col).float()), got
 
 
 # ------------------------------------------------------------------ ResAdd + RMSNorm
@@ -291,7 +298,7 @@ def _close(got: torch.Tensor, ref: torch.Tensor, what: str):
 @pytest.mark.parametrize("bm,variant", [(16, "stream"), (32, "tiled"), (64, "tiled"),
                                         (128, "tiled"), (64, "stream"), (64, "wide"),
                                         (128, "wide"), (64, "wide32"), (128, "wide32"),
-                                        (128, None)])
+                                        (64, "w512"), (128, "w512"), (128, None)])
 def test_grouped_gemms_small(gpu, bm, variant):
     say(f"grouped gemm small bm={bm} {variant}")
     T, E, H, I, k = 40, 16, 512, 256, 8
@@ -325,7 +332,7 @@ def test_grouped_gemm_full_width(gpu):
     ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
     act_ref = _gateup_ref(a, w13, ids, k, I, True)
     for bm, variant in ((16, "stream"), (32, "tiled"), (64, "wide"), (128, "wide"),
-                        (64, "wide32")):
+                        (64, "wide32"), (64, "w512"), (128, "w512")):
         say(f"grouped gemm full width bm={bm} {variant}")
         sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
         cfg = {"BLOCK_M": bm, "variant": variant}
