@@ -41,6 +41,46 @@ GLM52_DEV uint4 ldb(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }
 
+typedef __attribute__((address_space(3))) uint16_t lds_u16_t;
+
+// One direct 16-byte-per-lane load into LDS: lane l's 16 bytes land at byte `lds_base`
+// + 16 l (lds_base wave-uniform).  Issued from inline assembly so that the compiler's
+// wait-count pass, which loses track of these loads across the K loop's back edge and
+// would then drain every stage, leaves them alone: the kernel orders them with explicit
+// vmcnt waits before the barrier that publishes a stage.  m0 is set inside the statement
+// and nothing else in these kernels keeps a value in it.
+GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
+               :
+               : "s"(lds_base), "v"(gptr)
+               : "memory");
+}
+
+// The same load with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset:
+// lane l's 16 bytes at base + voff land at byte `lds_base` + 16 l.
+GLM52_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_base), "v"(voff), "s"(sbase)
+               : "memory");
+}
+
+// dma16s with the non-temporal hint: for streams read once (decode weights), so that they
+// do not displace cached data.
+GLM52_DEV void dma16s_nt(const void* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
+               :
+               : "s"(lds_base), "v"(voff), "s"(sbase)
+               : "memory");
+}
+
+GLM52_DEV uint32_t lds_addr(const uint16_t* p) {
+  return (uint32_t)(uintptr_t)(const lds_u16_t*)p;
+}
+
+// s_waitcnt vmcnt(n): every older vector-memory load of this wave has completed.
+#define GLM52_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(n) : "memory")
+
 struct GemmArgs {
   const uint16_t* A;
   int64_t sam;
@@ -81,5 +121,9 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 // The 512-row W tile mapping (moe_gemm_wide.hip): GLM52_EUNSUPPORTED for a block size or
 // shape it has no instance for.
 int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
+
+// The decode mapping that streams W as contiguous 1 KB row runs (moe_gemm_runs.hip): block
+// size 16; an optional extra expert (x_rows > 0) as in the stream mapping.
+int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
 
 }  // namespace glm52

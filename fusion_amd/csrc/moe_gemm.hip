@@ -355,6 +355,11 @@ int launch_tiled_bm(const GemmArgs& a, int capacity, hipStream_t st) {
 
 bool al16(const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; }
 
+// Output rows take 8-byte stores in the contiguous-run mapping.
+bool c_ok8(const void* c, int64_t stride) {
+  return (reinterpret_cast<uintptr_t>(c) & 7u) == 0 && (stride % 4) == 0;
+}
+
 // Bytes spanned by the A rows a layout can address: row f / a_div of every valid flat
 // index f, each K elements long at stride sa (the buffer range of the token loads).
 int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
@@ -368,7 +373,8 @@ int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
 // variant: 0 = choose (stream when BM == 16; 512-row W tiles when BM is 64 or 128, else the
 // 256-row wide mapping for shapes the 512-row one does not cover; tiled otherwise),
 // 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages, 5 = 512-row
-// W tiles (moe_gemm_wide.hip; block_m in {64, 128}).
+// W tiles (moe_gemm_wide.hip; block_m in {64, 128}), 6 = contiguous-run weight stream
+// (moe_gemm_runs.hip; block_m 16).  The default for block_m 16 is 6, else 1.
 extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                               int64_t stride_we, int64_t stride_wn, int gate_up_offset,
                               void* c, int64_t stride_cm, const float* topk_weights,
@@ -402,6 +408,13 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
   if (variant == 3 || variant == 4 || auto_wide) {
     g.stage_k = variant == 4 ? 32 : 64;
     return launch_wide(g, capacity, gated != 0, weighted, stream);
+  }
+  if (variant == 6 || (variant == 0 && block_m == 16)) {
+    // contiguous-run weight stream; shapes it has no instance for fall back to the stream
+    // mapping unless it was forced
+    const int rc = c_ok8(c, stride_cm) ? launch_runs(g, capacity, gated != 0, weighted, stream)
+                                       : GLM52_EUNSUPPORTED;
+    if (rc != GLM52_EUNSUPPORTED || variant == 6) return rc;
   }
   const bool use_stream = variant == 1 || (variant == 0 && block_m == 16);
   if (use_stream) {
@@ -450,6 +463,10 @@ extern "C" int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row
              shared_rows, a_bytes(num_valid_tokens, a_row_div, stride_am, k),
              a_bytes(shared_rows, 1, stride_as, k)};
   const bool weighted = topk_weights != nullptr;
+  if (c_ok8(c, stride_cm) && c_ok8(c_shared, stride_cs)) {
+    const int rc = launch_runs(g, capacity, gated != 0, weighted, stream);
+    if (rc != GLM52_EUNSUPPORTED) return rc;
+  }
   if (gated) return weighted ? launch_stream<true, true>(g, capacity, stream)
                              : launch_stream<true, false>(g, capacity, stream);
   return weighted ? launch_stream<false, true>(g, capacity, stream)

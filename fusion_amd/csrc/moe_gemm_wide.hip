@@ -53,37 +53,6 @@ GLM52_DEV int perm32(int n) { return ((n >> 2) & 1) * 16 + (n >> 3) * 4 + (n & 3
 // 1 KB of LDS (64 / CPR rows) in lane order, so each lane fetches the global chunk that
 // belongs at its slot; with BK = 64 a W row is fetched 128 B at a time.
 // ------------------------------------------------------------------------------------
-typedef __attribute__((address_space(3))) uint16_t lds_u16_t;
-
-// One direct 16-byte-per-lane load into LDS: lane l's 16 bytes land at byte `lds_base`
-// + 16 l (lds_base wave-uniform).  Issued from inline assembly so that the compiler's
-// wait-count pass, which loses track of these loads across the K loop's back edge and
-// would then drain every stage, leaves them alone: the kernel orders them with explicit
-// vmcnt waits before the barrier that publishes a stage.  m0 is set inside the statement
-// and nothing else in these kernels keeps a value in it.
-GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
-               :
-               : "s"(lds_base), "v"(gptr)
-               : "memory");
-}
-
-// The same load with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte offset:
-// lane l's 16 bytes at base + voff land at byte `lds_base` + 16 l.
-GLM52_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_base), "v"(voff), "s"(sbase)
-               : "memory");
-}
-
-GLM52_DEV uint32_t lds_addr(const uint16_t* p) {
-  return (uint32_t)(uintptr_t)(const lds_u16_t*)p;
-}
-
-// s_waitcnt vmcnt(n): every older vector-memory load of this wave has completed.
-#define GLM52_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(n) : "memory")
-
 // W row (0 <= n < 32) stored at LDS row perm32(n) of its group; the inverse.
 GLM52_DEV int iperm32(int r) { return ((r >> 2) & 3) * 8 + ((r >> 4) & 1) * 4 + (r & 3); }
 

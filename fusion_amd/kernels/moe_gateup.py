@@ -13,9 +13,10 @@ conventions (`glm52/kernels/REFERENCES.md:41-51`): A rows are gathered with
 `cfg["BLOCK_M"]` must equal the layout's block size (checked).  `cfg["variant"]` may
 force "stream" (weight-streaming decode mapping), "tiled" (register-staged LDS tiles),
 "wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages), "wide32"
-(the same with 32-k stages) or "w512" (512-row W tiles on the 32x32x16 MFMA, 32-k stages);
-by default BM = 16 streams, BM in {64, 128} runs "w512" (falling back to "wide" for
-shapes it does not cover) and BM = 32 "tiled".
+(the same with 32-k stages), "w512" (512-row W tiles on the 32x32x16 MFMA, 32-k stages) or
+"runs" (the decode weight stream read as contiguous 1 KB row runs through LDS); by default
+BM = 16 runs "runs" (falling back to "stream" for shapes it does not cover), BM in
+{64, 128} runs "w512" (falling back to "wide") and BM = 32 "tiled".
 """
 
 from __future__ import annotations
@@ -24,7 +25,8 @@ import torch
 
 from .. import _lib
 
-VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4, "w512": 5}
+VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4, "w512": 5,
+            "runs": 6}
 
 
 def check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m: int) -> int:
@@ -102,7 +104,9 @@ def smem_bytes(cfg: dict, fused: bool) -> int:
     """LDS bytes of the mapping this cfg selects (`moe_gateup.smem_bytes`'s question)."""
     bm = cfg["BLOCK_M"]
     variant = cfg.get("variant")
-    if variant == "stream" or (variant is None and bm == 16):
+    if variant == "runs" or (variant is None and bm == 16):
+        return 4 * 32 * 512 * 2 + 4 * 4 * 64 * 4
+    if variant == "stream":
         return 8192
     if variant == "w512" or (variant is None and bm in (64, 128)):
         return 4 * (512 + bm) * 32 * 2

@@ -331,7 +331,7 @@ def test_grouped_gemm_full_width(gpu):
     a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 5, gpu)
     ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
     act_ref = _gateup_ref(a, w13, ids, k, I, True)
-    for bm, variant in ((16, "stream"), (32, "tiled"), (64, "wide"), (128, "wide"),
+    for bm, variant in ((16, "stream"), (16, "runs"), (32, "tiled"), (64, "wide"), (128, "wide"),
                         (64, "wide32"), (64, "w512"), (128, "w512")):
         say(f"grouped gemm full width bm={bm} {variant}")
         sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
