@@ -32,6 +32,11 @@ SIGNATURES: dict[str, list] = {
     "glm52_moe_align": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "glm52_decode_front": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L,
                            _I, _I, _I, _I, _F, _F, _I, _I, _I, _P, _P, _P, _P, _P],
+    "glm52_decode_norm_logits": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I,
+                                 _F, _P],
+    "glm52_moe_gemm_route_shared": [_P, _L, _P, _I, _I, _I, _F, _I, _P, _L, _P, _L, _P, _P, _P,
+                                    _I, _P, _L, _P, _L, _L, _I, _P, _L, _P, _L, _P, _P, _L, _I,
+                                    _I, _P],
     "glm52_moe_gemm": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                        _I, _I, _P],
     "glm52_moe_gemm_shared": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I,

@@ -8,7 +8,9 @@ the routing computed live instead of frozen, and the tail fused):
     3. sigmoid + biased top-8   ids, weights                              router (launch 2)
     4. dispatch/align           sglang layout, count kept on the device  moe_align
                                 (T <= 16: 3 and 4 are one launch, router_topk_align;
-                                 T <= 4: 1-4 are one launch, decode_front)
+                                 T <= 4: 1-2 are one launch, decode_norm_logits, and
+                                 3-6 are one launch, moe_gemm_route_shared, which
+                                 derives the routing from the logits in every workgroup)
     5. routed w13 + SwiGLU      act[8T, I]                                moe_gemm (gated)
     6. shared w13 + SwiGLU      act_s[T, I]                               moe_gemm (gated, E=1)
     7. routed w2 (weighted)     Y[8T, H] = w * (act . w2^T)               moe_gemm
@@ -29,8 +31,8 @@ import torch
 
 from . import config as C
 from . import _lib
-from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_front_into, moe_align_block_size_into,
-                       topk_align_into)
+from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
+                       moe_align_block_size_into, route_gateup_shared_into, topk_align_into)
 from .kernels import add_rmsnorm as KN
 from .kernels import norm_router as KR
 from .kernels.moe_gateup import moe_gemm, moe_gemm_shared
@@ -109,15 +111,14 @@ class MoEBlock:
         self.cfg_r = {"BLOCK_M": self.bm, "variant": variant}
         self.cfg_s = {"BLOCK_M": self.sbm, "variant": variant}
         # decode: the [E, H] gate rows feed the one-row-per-wave router, and top-k plus
-        # the dispatch layout run as one single-workgroup launch; at T <= 4 the whole
-        # front end (norm, router, top-k, layout) is one launch
+        # the dispatch layout run as one single-workgroup launch; at T <= 4 norm and
+        # logits are one launch and the routing is derived inside the w13 launch
         self.decode = T <= 16 and T * self.topk <= 256
-        self.front_fused = T <= DECODE_FRONT_MAX_T
-        self.gate_rows = wgt.t().contiguous() if self.decode else None  # [E, H]
-        self.wgt_rows = self.gate_rows.t() if self.decode else None  # its [H, E] view
-        self.counter = torch.zeros(1, dtype=torch.int32, device=dev)
         # weight-streaming decode runs the shared expert inside the routed launches
         self.shared_fused = self.bm == 16
+        self.front_fused = T <= DECODE_FRONT_MAX_T and self.shared_fused
+        self.gate_rows = wgt.t().contiguous() if self.decode else None  # [E, H]
+        self.wgt_rows = self.gate_rows.t() if self.decode else None  # its [H, E] view
         need = KR.workspace_bytes(T, H, E)
         self.router_ws = torch.empty(max(need, 8), dtype=torch.uint8, device=dev)
         self.cfg_topk = {"correction_bias": bias, "scale": scale, "workspace": self.router_ws}
@@ -126,9 +127,9 @@ class MoEBlock:
     # ---- the chain -------------------------------------------------------------------
     def front_end(self, x, r):
         if self.front_fused:
-            decode_front_into(x, r, self.w_norm, self.h, self.y, self.gate_rows,
-                              dict(self.cfg_topk, eps=self.eps), self.logits, self.topw,
-                              self.topi, self.bm, self.sti, self.eids, self.ntp, self.counter)
+            # norm + logits here; the routing is derived inside the w13 launch (experts())
+            decode_norm_logits_into(x, r, self.w_norm, self.h, self.y, self.gate_rows,
+                                    self.logits, self.eps)
             return
         KN.fused_add_rmsnorm(x, r, self.w_norm, self.h, self.y, {"eps": self.eps})
         if self.decode:
@@ -142,9 +143,14 @@ class MoEBlock:
 
     def experts(self):
         T, H, I, R = self.T, self.H, self.I, self.T * self.topk
-        if self.shared_fused:
+        if self.front_fused:
+            route_gateup_shared_into(self.logits, self.cfg_topk, self.topw, self.topi, self.sti,
+                                     self.eids, self.ntp, self.y, self.w13, self.act, self.y,
+                                     self.w13s, self.act_s)
+        elif self.shared_fused:
             moe_gemm_shared(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids,
                             self.ntp, R, I, I, True, self.cfg_r, self.y, self.w13s, self.act_s)
+        if self.shared_fused:
             moe_gemm_shared(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti,
                             self.eids, self.ntp, R, H, 0, False, self.cfg_r, self.act_s, self.w2s,
                             self.s_out)

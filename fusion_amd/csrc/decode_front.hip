@@ -16,7 +16,9 @@
 // wave dots its row with the staged rows.  The workgroups publish their logits, then count themselves
 // on a device-scope counter; the last one to arrive runs the top-k of every token and
 // builds the layout, then resets the counter to zero for the next launch.  The counter
-// is the only state and must be zero before the first launch.
+// is the only state and must be zero before the first launch.  glm52_decode_norm_logits
+// runs the kernel without that last step (no counter): the routed decode GEMM derives the
+// routing from the logits itself.
 #include "select.h"
 
 using namespace glm52;
@@ -27,6 +29,7 @@ constexpr int kTmax = 4;
 constexpr int kHmax = 8192;
 constexpr int kChunks = kHmax / 8 / 256;  // 16-byte chunks per thread of one row
 
+template <bool TAIL>
 __global__ __launch_bounds__(256) void decode_front_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ wn, uint16_t* __restrict__ h_out, uint16_t* __restrict__ y_out,
@@ -151,6 +154,7 @@ __global__ __launch_bounds__(256) void decode_front_kernel(
   }
 
   // ---- 3. the last workgroup to arrive selects and builds the layout -----------------
+  if (!TAIL) return;
   __threadfence();  // publish this workgroup's logits (and h, y) device-wide
   __syncthreads();
   if (tid == 0) is_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
@@ -189,11 +193,35 @@ extern "C" int glm52_decode_front(const void* x, int64_t stride_x, const void* r
     return GLM52_EINVAL;
   const int64_t need = (int64_t)T * topk + (int64_t)E * (block_m - 1);
   if (capacity < need || (capacity % block_m)) return GLM52_EINVAL;
-  decode_front_kernel<<<(E + 3) / 4, 256, 0, stream>>>(
+  decode_front_kernel<true><<<(E + 3) / 4, 256, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res),
       static_cast<const uint16_t*>(w_norm), static_cast<uint16_t*>(h1), static_cast<uint16_t*>(y),
       stride_x, stride_r, stride_h, stride_y, static_cast<const uint16_t*>(gate), stride_g, bias,
       logits, stride_l, topw, stride_w, topi, stride_i, T, H, E, topk, eps, scale, norm_prob,
       block_m, capacity, sorted_token_ids, expert_ids, num_tokens_post_padded, counter);
+  GLM52_RETURN_LAUNCH();
+}
+
+// The first part of glm52_decode_front alone: ResAdd + RMSNorm and the router logits of
+// T <= 4 tokens in one launch, no top-k (glm52_moe_gemm_route_shared derives the routing).
+extern "C" int glm52_decode_norm_logits(const void* x, int64_t stride_x, const void* res,
+                                        int64_t stride_r, const void* w_norm, void* h1,
+                                        int64_t stride_h, void* y, int64_t stride_y,
+                                        const void* gate, int64_t stride_g, float* logits,
+                                        int64_t stride_l, int T, int H, int E, float eps,
+                                        hipStream_t stream) {
+  if (T < 1 || T > kTmax || H <= 0 || H > kHmax || (H % 8) || E <= 0 || E > kMaxE || (E % 4))
+    return GLM52_EINVAL;
+  if (!x || !res || !w_norm || !h1 || !y || !gate || !logits) return GLM52_EINVAL;
+  if (!al16(x) || !al16(res) || !al16(w_norm) || !al16(h1) || !al16(y) || !al16(gate) ||
+      (stride_x % 8) || (stride_r % 8) || (stride_h % 8) || (stride_y % 8) || (stride_g % 8) ||
+      stride_g < H || stride_l < E)
+    return GLM52_EINVAL;
+  decode_front_kernel<false><<<(E + 3) / 4, 256, 0, stream>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res),
+      static_cast<const uint16_t*>(w_norm), static_cast<uint16_t*>(h1), static_cast<uint16_t*>(y),
+      stride_x, stride_r, stride_h, stride_y, static_cast<const uint16_t*>(gate), stride_g, nullptr,
+      logits, stride_l, nullptr, 0, nullptr, 0, T, H, E, 1, eps, 1.f, 1, 16, 0, nullptr, nullptr,
+      nullptr, nullptr);
   GLM52_RETURN_LAUNCH();
 }

@@ -112,6 +112,22 @@ struct GemmArgs {
   int x_rows;
   int a_bytes;   // stream mapping: bytes of A (and of Ax) its token rows span
   int ax_bytes;
+  // contiguous-run mapping in routing mode (decode, T <= 4 tokens): the layout is not read
+  // from sti / eids / ntp but derived in every workgroup from the router logits; the
+  // routing (ids, weights) and the layout are written out for the kernels that follow
+  const float* r_logits;
+  int64_t r_sl;
+  const float* r_bias;
+  int r_T, r_E, r_topk, r_norm_prob;
+  float r_scale;
+  float* r_topw;
+  int64_t r_stw;
+  int32_t* r_topi;
+  int64_t r_sti;
+  int32_t* r_sorted;
+  int32_t* r_eids;
+  int32_t* r_ntp;
+  int r_capacity;
 };
 
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
@@ -123,7 +139,9 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
 
 // The decode mapping that streams W as contiguous 1 KB row runs (moe_gemm_runs.hip): block
-// size 16; an optional extra expert (x_rows > 0) as in the stream mapping.
-int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
+// size 16; an optional extra expert (x_rows > 0) as in the stream mapping; `route`: the
+// routing mode (gated, unweighted, with the extra expert).
+int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, bool route,
+                hipStream_t st);
 
 }  // namespace glm52

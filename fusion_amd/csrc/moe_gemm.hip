@@ -412,7 +412,7 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
   if (variant == 6 || (variant == 0 && block_m == 16)) {
     // contiguous-run weight stream; shapes it has no instance for fall back to the stream
     // mapping unless it was forced
-    const int rc = c_ok8(c, stride_cm) ? launch_runs(g, capacity, gated != 0, weighted, stream)
+    const int rc = c_ok8(c, stride_cm) ? launch_runs(g, capacity, gated != 0, weighted, false, stream)
                                        : GLM52_EUNSUPPORTED;
     if (rc != GLM52_EUNSUPPORTED || variant == 6) return rc;
   }
@@ -464,13 +464,51 @@ extern "C" int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row
              a_bytes(shared_rows, 1, stride_as, k)};
   const bool weighted = topk_weights != nullptr;
   if (c_ok8(c, stride_cm) && c_ok8(c_shared, stride_cs)) {
-    const int rc = launch_runs(g, capacity, gated != 0, weighted, stream);
+    const int rc = launch_runs(g, capacity, gated != 0, weighted, false, stream);
     if (rc != GLM52_EUNSUPPORTED) return rc;
   }
   if (gated) return weighted ? launch_stream<true, true>(g, capacity, stream)
                              : launch_stream<true, false>(g, capacity, stream);
   return weighted ? launch_stream<false, true>(g, capacity, stream)
                   : launch_stream<false, false>(g, capacity, stream);
+}
+
+// Decode (T <= 4 tokens): the router's biased top-k and the dispatch layout (block_m 16),
+// derived from the logits inside the routed w13 + SwiGLU launch with the shared expert --
+// glm52_router_topk_align followed by glm52_moe_gemm_shared (gated), in one launch with no
+// grid-wide wait (moe_gemm_runs.hip).
+extern "C" int glm52_moe_gemm_route_shared(
+    const float* logits, int64_t stride_l, const float* bias, int T, int E, int topk,
+    float scale, int norm_prob, float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i,
+    int32_t* sorted_token_ids, int32_t* expert_ids, int32_t* num_tokens_post_padded,
+    int capacity, const void* a, int64_t stride_am, const void* w, int64_t stride_we,
+    int64_t stride_wn, int gate_up_offset, void* c, int64_t stride_cm, const void* a_shared,
+    int64_t stride_as, const void* w_shared, void* c_shared, int64_t stride_cs, int n_out,
+    int k, hipStream_t stream) {
+  if (!logits || !topw || !topi || !sorted_token_ids || !expert_ids || !num_tokens_post_padded ||
+      !a || !w || !c || !a_shared || !w_shared || !c_shared)
+    return GLM52_EINVAL;
+  if (T < 1 || T > 4 || E < 1 || topk < 1 || topk > 8 || topk > E || stride_l < E ||
+      stride_w < topk || stride_i < topk || capacity < 0 || (capacity % 16))
+    return GLM52_EINVAL;
+  // logits rows and the bias are loaded 16 bytes per lane
+  if (!al16(logits) || (stride_l % 4) || (bias && !al16(bias))) return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % 16) != 0 || k <= 0 || (k % 256) != 0 || gate_up_offset < n_out)
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w) || !al16(w_shared) || !al16(a_shared) || (stride_am % 8) ||
+      (stride_as % 8) || (stride_we % 8) || (stride_wn % 8) || !c_ok8(c, stride_cm) ||
+      !c_ok8(c_shared, stride_cs))
+    return GLM52_EINVAL;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, topk,
+             static_cast<const uint16_t*>(w), stride_we, stride_wn, gate_up_offset,
+             static_cast<uint16_t*>(c), stride_cm, nullptr, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, 16, n_out, k, T * topk, 4, 64,
+             static_cast<const uint16_t*>(a_shared), stride_as,
+             static_cast<const uint16_t*>(w_shared), static_cast<uint16_t*>(c_shared), stride_cs,
+             T, 0, 0,
+             logits, stride_l, bias, T, E, topk, norm_prob, scale, topw, stride_w, topi, stride_i,
+             sorted_token_ids, expert_ids, num_tokens_post_padded, capacity};
+  return launch_runs(g, capacity, true, false, true, stream);
 }
 
 // Self-test of the MFMA result layouts this library assumes, for the bf16 16x16x32, the fp64

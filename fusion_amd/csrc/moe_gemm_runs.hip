@@ -8,11 +8,12 @@
 // loaded in runs straight into LDS (`global_load_lds_dwordx4`, one 1 KB row run per
 // instruction, non-temporal: W is read once) and read back from LDS in MFMA layout.
 //
-// Item.  One 16-row slice of the layout (an expert's block of BM = 16 slots, or 16 tokens of
-// the extra expert) times 16 W rows: gated, 8 `gate` rows and the matching 8 `up` rows (8
-// outputs); plain, 16 rows (16 outputs).  The four waves split K: wave w multiplies k-steps
-// w*4 .. +3 of every 512-k stage with `v_mfma_f32_16x16x32_bf16` (W rows x tokens) and the
-// partial sums meet in LDS in a fixed order at the item's end.
+// Item.  One 16-row slice (an expert's block of BM = 16 layout slots, or 16 tokens of the
+// extra expert) times 16 W rows: gated, 8 `gate` rows and the matching 8 `up` rows (8
+// outputs); plain, 16 rows (16 outputs).  The extra expert's slices come first.  The four
+// waves split K: wave w multiplies k-steps w*4 .. +3 of every 512-k stage with
+// `v_mfma_f32_16x16x32_bf16` (W rows x tokens) and the partial sums meet in LDS in a fixed
+// order at the item's end.
 //
 // Pipeline.  A stage is the 512-k run of the item's 16 W rows and its real token rows (up
 // to 16; the rows of padding slots are not loaded, and whatever their LDS rows hold only
@@ -20,10 +21,26 @@
 // buffers with three in flight, and the ring runs across item boundaries, so every
 // workgroup streams continuously.  Each wave counts the loads it issued per stage, and a
 // stage is waited for with the count of the two newer stages; stages past the workgroup's
-// last one re-read its last stage into the free buffer.  Staged row R keeps global 16-byte
-// chunk c at chunk c ^ (R & 15): the 16 lanes of an operand read hit 16 distinct bank
-// groups.
+// last one re-read its last stage into the free buffer.  The layout entries an item needs
+// (expert, token ids, routing weights) are read with scalar loads, which do not share the
+// vector-memory counter, so reading them never drains the weight loads in flight; the
+// epilogue takes the token ids and weights from a small LDS ring.  Staged row R keeps
+// global 16-byte chunk c at chunk c ^ (R & 15): the 16 lanes of an operand read hit 16
+// distinct bank groups.
+//
+// Routing mode (decode, T <= 4 tokens, gated, with the shared expert as the extra one).
+// The layout is not read but derived: every workgroup computes the biased top-k of the T
+// tokens from the router logits (the rule of `glm52/reference.py:62-79` as in select.h; an
+// expert's slot is the number of experts that beat it, counted by its own thread) and the
+// sglang layout of the selected ids (`glm52/reference.py:85-128`; with T <= 4 no expert gets
+// more than 16 ids, so each selected expert owns one block, in ascending expert order, its
+// ids in ascending flat order) into LDS: the logits and the bias are loaded straight into
+// LDS ahead of the loads of its first item -- a shared-expert item, which needs no
+// routing -- and the routing waits for them alone.  Workgroup 0 writes the ids and weights; all
+// workgroups share writing the layout, so the kernels that follow read the same tensors as
+// after glm52_router_topk_align.  Nothing here waits on another workgroup.
 #include "moe_gemm.h"
+#include "select.h"
 
 using namespace glm52;
 
@@ -33,11 +50,41 @@ constexpr int KS = 512;            // k per stage: one 1 KB run of every staged 
 constexpr int NSTAGE = 4;
 constexpr int SROWS = 32;          // 16 W rows + 16 token rows
 constexpr int SELEM = SROWS * KS;  // elements per stage
+constexpr int RT = 4;              // routing mode: at most 4 tokens
+constexpr int RSLOT = RT * 8;      // ... and at most 32 routed ids
+constexpr int NMETA = 4;           // items whose token ids / weights are kept for the epilogue
 
-template <bool GATED, bool WEIGHTED>
+struct RouteLds {
+  float logits[RT][kMaxE];  // the T tokens' logits and the bias, loaded straight into LDS
+  float bias[kMaxE];
+  uint64_t key[RT][kMaxE];  // selection keys as unique ordered integers, and the scores
+  float score[RT][kMaxE];
+  float sel_s[RT][8];
+  int sel_i[RT][8];
+  int ids[RSLOT];
+  int blk_e[RSLOT];      // expert of layout block b
+  int blk_n[RSLOT];      // its id count (<= RT)
+  int blk_f[RSLOT][RT];  // its flat ids, ascending
+  int nblk;
+};
+
+// A wave-uniform 32-bit load through the scalar cache (lgkmcnt, not vmcnt).
+GLM52_DEV int sload_i32(const void* base, int idx) {
+  int v;
+  asm volatile("s_load_dword %0, %1, %2\n\ts_waitcnt lgkmcnt(0)"
+               : "=s"(v)
+               : "s"(base), "s"(idx * 4)
+               : "memory");
+  return v;
+}
+
+template <bool GATED, bool WEIGHTED, bool ROUTE>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
   __shared__ float red[4][4][kWave];
+  __shared__ int meta_tok[NMETA][16];    // flat ids of an item's token rows
+  __shared__ float meta_w[NMETA][16];    // their routing weights (weighted)
+  __shared__ RouteLds rs;
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -46,25 +93,27 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   const int r16 = lane % 16, g = lane / 16;
 
   constexpr int NOC = GATED ? 8 : 16;  // outputs per item
-  const int num_m = *p.ntp / 16;
   const int xm = (p.x_rows + 15) / 16;
   const int num_n = p.n_out / NOC;
-  const int items = (num_m + xm) * num_n;
+  const int x_items = xm * num_n;  // the extra expert's items come first
   const int nks = p.K / KS;
-  if ((int)blockIdx.x >= items) return;
-  const int total = ((items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x) * nks;
+  int num_m = ROUTE ? 0 : sload_i32(p.ntp, 0) / 16;
+  int items = (xm + num_m) * num_n;
   const uint32_t ring_base = lds_addr(ring);
 
   // ---- load side: the wave's 4 W rows and its real token rows (da_n of 4) of the item
-  // being loaded -------------------------------------------------------------------------
+  // being loaded; the item's token ids (and weights) go to the LDS ring for its epilogue
   const uint16_t* dw[4];
   const uint16_t* da[4];
   int da_n = 0;
   auto dma_setup = [&](int it) {
     const int m = it / num_n;
     const int n0 = (it % num_n) * NOC;
-    const bool extra = m >= num_m;
-    const uint16_t* wbase = extra ? p.Wx : p.W + (int64_t)p.eids[m] * p.swe;
+    const bool extra = m < xm;
+    const int slot = (it / (int)gridDim.x) % NMETA;
+    int e = 0;
+    if (!extra) e = ROUTE ? __builtin_amdgcn_readfirstlane(rs.blk_e[m - xm]) : sload_i32(p.eids, m - xm);
+    const uint16_t* wbase = extra ? p.Wx : p.W + (int64_t)e * p.swe;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = wvu * 4 + i;  // W tile row
@@ -75,14 +124,26 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tr = wvu * 4 + i;  // token row of the slice; real rows fill a prefix
+      int f;
+      bool ok;
       if (extra) {
-        const int tok = (m - num_m) * 16 + tr;
-        da[i] = p.Ax + (int64_t)(tok < p.x_rows ? tok : 0) * p.sax;
-        da_n += tok < p.x_rows ? 1 : 0;
+        f = m * 16 + tr;
+        ok = f < p.x_rows;
+        da[i] = p.Ax + (int64_t)(ok ? f : 0) * p.sax;
       } else {
-        const int tok = __builtin_amdgcn_readfirstlane(p.sti[m * 16 + tr]);
-        da[i] = p.A + (int64_t)(tok < p.num_valid ? tok / p.a_div : 0) * p.sam;
-        da_n += tok < p.num_valid ? 1 : 0;
+        if constexpr (ROUTE)
+          f = __builtin_amdgcn_readfirstlane(tr < rs.blk_n[m - xm] ? rs.blk_f[m - xm][tr] : p.num_valid);
+        else
+          f = sload_i32(p.sti, (m - xm) * 16 + tr);
+        ok = f < p.num_valid;
+        da[i] = p.A + (int64_t)(ok ? f / p.a_div : 0) * p.sam;
+      }
+      da_n += ok ? 1 : 0;
+      float w = 1.f;
+      if (WEIGHTED && !extra && ok) w = __builtin_bit_cast(float, sload_i32(p.topw, f));
+      if (lane == 0) {
+        meta_tok[slot][tr] = ok ? f : -1;
+        meta_w[slot][tr] = w;
       }
     }
   };
@@ -114,6 +175,130 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     }
   };
 
+  // ---- routing mode: the top-k of every token and the layout, into LDS ------------------
+  // Loads of the logits (wave t: token t) and the bias (wave 0) straight into LDS, issued
+  // before the first item's stages so that they land first; returns the loads issued.
+  auto route_load = [&]() {
+    int n = 0;
+    if (wvu < p.r_T) {
+      if (4 * lane < p.r_E)
+        dma16s(p.r_logits + (int64_t)wvu * p.r_sl, (uint32_t)(lane * 16),
+               lds_addr(reinterpret_cast<const uint16_t*>(&rs.logits[wvu][0])));
+      ++n;
+    }
+    if (wvu == 0 && p.r_bias) {
+      if (4 * lane < p.r_E)
+        dma16s(p.r_bias, (uint32_t)(lane * 16), lds_addr(reinterpret_cast<const uint16_t*>(&rs.bias[0])));
+      ++n;
+    }
+    return n;
+  };
+  auto route = [&]() {
+    const int T = p.r_T, E = p.r_E, topk = p.r_topk;
+    const bool active = wv < T;
+    // thread tid owns expert tid: its score and key for every token (the rule of topk_keys).
+    // The key goes to LDS as one integer that orders like the selection order: the float
+    // key mapped to an unsigned integer of the same order (-0 taken as +0, so that equal
+    // keys stay equal) above the complement of the expert index, so that a larger key, or
+    // an equal key at a lower index, is a larger integer.  A comparison is then a single
+    // vector compare: boolean combinations of compares would run on the scalar unit, each
+    // waiting on the vector unit's result.
+    for (int t = 0; t < T; ++t) {
+      if (tid < E) {
+        const float sc = (float)(1.0 / (1.0 + exp(-(double)rs.logits[t][tid])));
+        float k = p.r_bias ? sc + rs.bias[tid] : sc;
+        k = (k != k) ? -INFINITY : (k == 0.f ? 0.f : k);
+        const uint32_t b = __builtin_bit_cast(uint32_t, k);
+        const uint32_t ord = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+        rs.key[t][tid] = ((uint64_t)ord << 32) | (uint32_t)(~tid);
+        rs.score[t][tid] = sc;
+      }
+    }
+    __syncthreads();
+    // slot of expert tid = the number of experts whose key integer is larger
+    for (int t = 0; t < T; ++t) {
+      if (tid < E) {
+        const uint64_t k = rs.key[t][tid];
+        int rank = 0;
+#pragma unroll 8
+        for (int e2 = 0; e2 < E; e2 += 2) {
+          const ulonglong2 q = *reinterpret_cast<const ulonglong2*>(&rs.key[t][e2]);
+          rank += q.x > k ? 1 : 0;
+          rank += q.y > k ? 1 : 0;
+        }
+        if (rank < topk) {
+          rs.sel_i[t][rank] = tid;
+          rs.sel_s[t][rank] = rs.score[t][tid];
+        }
+      }
+    }
+    __syncthreads();
+    if (active && lane < topk) {
+      float w;
+      int id;
+      topk_weight(rs.sel_s[wv], rs.sel_i[wv], topk, p.r_scale, p.r_norm_prob, &w, &id);
+      rs.ids[wv * topk + lane] = id;
+      if (blockIdx.x == 0) {
+        p.r_topw[(int64_t)wv * p.r_stw + lane] = w;
+        p.r_topi[(int64_t)wv * p.r_sti + lane] = id;
+      }
+    }
+    __syncthreads();
+    const int numel = T * topk;
+    if (wv == 0) {
+      // one block per distinct expert, in expert order; ids of one expert in flat order.
+      // Lane f (flat id f) counts with single compares: ids of a smaller expert (below),
+      // ids before it in (expert, flat) order (pos), and ids of its expert (same); then the
+      // distinct experts below its own, counting only the first id of each expert.
+      const int e = lane < numel ? rs.ids[lane] : kMaxE;
+      const int c = e * 64 + lane;
+      int below = 0, pos = 0, upto = 0;
+      for (int j = 0; j < numel; ++j) {
+        const int ej = rs.ids[j];
+        below += ej < e ? 1 : 0;
+        upto += ej <= e ? 1 : 0;
+        pos += ej * 64 + j < c ? 1 : 0;
+      }
+      const int earlier_same = pos - below;
+      const uint64_t firsts = __ballot(lane < numel && earlier_same == 0);
+      int distinct_below = 0;
+      for (int j = 0; j < numel; ++j) {
+        const int ej = rs.ids[j];
+        const int fk = ((firsts >> j) & 1ull) ? ej : kMaxE;  // wave-uniform select
+        distinct_below += fk < e ? 1 : 0;
+      }
+      if (lane < numel) {
+        rs.blk_f[distinct_below][earlier_same] = lane;
+        if (earlier_same == 0) {
+          rs.blk_e[distinct_below] = e;
+          rs.blk_n[distinct_below] = upto - below;
+        }
+      }
+      if (lane == 0) rs.nblk = __popcll(firsts);
+    }
+    __syncthreads();
+    // the layout tensors, split over the workgroups: slot s of sorted_token_ids holds the
+    // flat id of slot s % 16 of block s / 16, or the sentinel numel; expert_ids[b] the
+    // expert of block b, or -1 past the last block
+    const int nblk = rs.nblk;
+    const int cap = p.r_capacity;
+    const int nent = cap + cap / 16;
+    const int per = (nent + (int)gridDim.x - 1) / (int)gridDim.x;
+    const int q1 = min(nent, ((int)blockIdx.x + 1) * per);
+    for (int q = (int)blockIdx.x * per + tid; q < q1; q += 256) {
+      if (q < cap) {
+        const int b = q / 16, j = q % 16;
+        p.r_sorted[q] = (b < nblk && j < rs.blk_n[b]) ? rs.blk_f[b][j] : numel;
+      } else {
+        const int b = q - cap;
+        p.r_eids[b] = b < nblk ? rs.blk_e[b] : -1;
+      }
+    }
+    if (blockIdx.x == 0 && tid == 0) p.r_ntp[0] = nblk * 16;
+    num_m = __builtin_amdgcn_readfirstlane(nblk);
+    items = (xm + num_m) * num_n;
+  };
+
   // ---- multiply side ------------------------------------------------------------------
   auto compute = [&](int buf, floatx4_t acc) {
     const uint16_t* sb = ring + buf * SELEM;
@@ -133,16 +318,10 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     if (wv != 0) return;
     const int m = it / num_n;
     const int n0 = (it % num_n) * NOC;
-    const bool extra = m >= num_m;
-    int tok;
-    bool ok;
-    if (extra) {
-      tok = (m - num_m) * 16 + r16;
-      ok = tok < p.x_rows;
-    } else {
-      tok = p.sti[m * 16 + r16];
-      ok = tok < p.num_valid;
-    }
+    const bool extra = m < xm;
+    const int slot = (it / (int)gridDim.x) % NMETA;
+    const int tok = meta_tok[slot][r16];
+    if (tok < 0) return;
     float v[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -154,16 +333,13 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         u[i] = ((red[0][i][lu] + red[1][i][lu]) + red[2][i][lu]) + red[3][i][lu];
-      if (!ok || g >= 2) return;
+      if (g >= 2) return;
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = silu_mul(v[i], u[i]);
-    } else {
-      if (!ok) return;
-      if (WEIGHTED && !extra) {
-        const float w = p.topw[tok];
+    } else if (WEIGHTED && !extra) {
+      const float w = meta_w[slot][r16];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = v[i] * w;
-      }
+      for (int i = 0; i < 4; ++i) v[i] = v[i] * w;
     }
     uint16_t* dst = extra ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm;
     uint2 o;
@@ -172,15 +348,56 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     *reinterpret_cast<uint2*>(dst + n0 + 4 * g) = o;
   };
 
-  // loads issued by this wave for the two stages after the one being waited for
-  int n1, n2;
-  dma_setup(d_item);
-  issue(d_s, 0);
-  dma_advance();
-  n1 = issue(d_s, 1);
-  dma_advance();
-  n2 = issue(d_s, 2);
-  dma_advance();
+  // prologue: the first three stages of the first item.  In routing mode the logits are
+  // loaded first and a first item of the extra expert is issued before the routing (which
+  // waits only for the logits); a routed first item after it.
+  int n0 = 0, n1 = 0, n2 = 0;
+  auto prologue = [&]() {
+    dma_setup(d_item);
+    n0 = issue(d_s, 0);
+    dma_advance();
+    n1 = issue(d_s, 1);
+    dma_advance();
+    n2 = issue(d_s, 2);
+    dma_advance();
+  };
+  const bool first_extra = (int)blockIdx.x < x_items;
+  if (!ROUTE) {
+    if ((int)blockIdx.x >= items) return;
+    prologue();
+  } else {
+    route_load();
+    if (first_extra) {
+      prologue();
+      // the logits landed (this wave's; every wave's after the routing's first barrier):
+      // at most the prologue's loads are still in flight
+      switch (n0 + n1 + n2) {
+        case 12: GLM52_WAIT_VMCNT(12); break;
+        case 13: GLM52_WAIT_VMCNT(13); break;
+        case 14: GLM52_WAIT_VMCNT(14); break;
+        case 15: GLM52_WAIT_VMCNT(15); break;
+        case 16: GLM52_WAIT_VMCNT(16); break;
+        case 17: GLM52_WAIT_VMCNT(17); break;
+        case 18: GLM52_WAIT_VMCNT(18); break;
+        case 19: GLM52_WAIT_VMCNT(19); break;
+        case 20: GLM52_WAIT_VMCNT(20); break;
+        case 21: GLM52_WAIT_VMCNT(21); break;
+        case 22: GLM52_WAIT_VMCNT(22); break;
+        case 23: GLM52_WAIT_VMCNT(23); break;
+        default: GLM52_WAIT_VMCNT(24); break;
+      }
+    } else {
+      GLM52_WAIT_VMCNT(0);
+    }
+    __syncthreads();
+    route();
+    if (!first_extra) {
+      if ((int)blockIdx.x >= items) return;
+      prologue();
+    }
+  }
+  const int total = ((items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x) * nks;
+
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
   int c_item = blockIdx.x, c_s = 0;
 #pragma unroll 1
@@ -213,22 +430,31 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   GLM52_WAIT_VMCNT(0);  // the re-reads past the last stage land before the workgroup ends
 }
 
-template <bool GATED, bool WEIGHTED>
+template <bool GATED, bool WEIGHTED, bool ROUTE>
 int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
   constexpr int NOC = GATED ? 8 : 16;
   if (a.BM != 16 || (a.n_out % NOC) || (a.K % KS) || a.K / KS < 1) return GLM52_EUNSUPPORTED;
+  if (ROUTE && (a.x_rows < 1 || a.r_T < 1 || a.r_T > RT || a.r_topk < 1 || a.r_topk > 8 ||
+                a.r_E < a.r_topk || a.r_E > kMaxE || (a.r_E % 4) ||
+                a.r_capacity < a.r_T * a.r_topk + a.r_E * 15 || (a.r_capacity % 16)))
+    return GLM52_EINVAL;
   const int items_max = (capacity / 16 + (a.x_rows + 15) / 16) * (a.n_out / NOC);
   int grid = items_max < 256 ? items_max : 256;
   if (grid < 1) grid = 1;
-  moe_gemm_runs_kernel<GATED, WEIGHTED><<<grid, 256, 0, st>>>(a);
+  moe_gemm_runs_kernel<GATED, WEIGHTED, ROUTE><<<grid, 256, 0, st>>>(a);
   GLM52_RETURN_LAUNCH();
 }
 
 }  // namespace
 
 namespace glm52 {
-int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st) {
-  if (gated) return weighted ? launch_runs_t<true, true>(a, capacity, st) : launch_runs_t<true, false>(a, capacity, st);
-  return weighted ? launch_runs_t<false, true>(a, capacity, st) : launch_runs_t<false, false>(a, capacity, st);
+int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, bool route,
+                hipStream_t st) {
+  if (route) {
+    if (!gated || weighted) return GLM52_EUNSUPPORTED;
+    return launch_runs_t<true, false, true>(a, capacity, st);
+  }
+  if (gated) return weighted ? launch_runs_t<true, true, false>(a, capacity, st) : launch_runs_t<true, false, false>(a, capacity, st);
+  return weighted ? launch_runs_t<false, true, false>(a, capacity, st) : launch_runs_t<false, false, false>(a, capacity, st);
 }
 }  // namespace glm52

@@ -26,18 +26,30 @@ GLM52_DEV void load_bias(const float* __restrict__ bias, int E, float bv[4]) {
 }
 
 // Stage 1 (every lane): scores and keys of the token's experts lane + 64 j.
+// The fp64 sigmoid is long code; it is kept in one copy inside a rolled loop, because
+// right after a cache flush every instruction line of a kernel is fetched from HBM and
+// four unrolled copies cost microseconds of fetch latency.
 GLM52_DEV void topk_keys(const float lg[4], const float bv[4], bool has_bias, int E, bool active,
                          float sc[4], float key[4]) {
   const int lane = threadIdx.x % kWave;
+  float s4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int j = 0; j < 4; ++j) {
+    const float x = j == 0 ? lg[0] : j == 1 ? lg[1] : j == 2 ? lg[2] : lg[3];
+    const float s = (float)(1.0 / (1.0 + exp(-(double)x)));
+    s4[0] = j == 0 ? s : s4[0];
+    s4[1] = j == 1 ? s : s4[1];
+    s4[2] = j == 2 ? s : s4[2];
+    s4[3] = j == 3 ? s : s4[3];
+  }
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + j * kWave;
     key[j] = -INFINITY;
     sc[j] = 0.f;
     if (active && e < E) {
-      const float s = (float)(1.0 / (1.0 + exp(-(double)lg[j])));
-      sc[j] = s;
-      const float k = has_bias ? s + bv[j] : s;
+      sc[j] = s4[j];
+      const float k = has_bias ? s4[j] + bv[j] : s4[j];
       key[j] = (k != k) ? -INFINITY : k;
     }
   }

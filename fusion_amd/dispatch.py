@@ -107,3 +107,49 @@ def decode_front_into(x, r, w_norm, h1, y, gate_rows, cfg, logits, topw, topi, b
         _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), _lib.ptr(counter),
         _lib.stream(),
     )
+
+
+def decode_norm_logits_into(x, r, w_norm, h1, y, gate_rows, logits, eps: float = 1e-5):
+    """ResAdd + RMSNorm and the router logits of T <= 4 tokens in one launch (the first
+    part of `decode_front_into`): `fused_add_rmsnorm` -> `router_gemm`, bit-identical."""
+    _lib.require_gpu(x, r, w_norm, h1, y, gate_rows, logits)
+    T, H = x.shape
+    E = gate_rows.shape[0]
+    if gate_rows.shape[1] != H or gate_rows.stride(1) != 1 or gate_rows.dtype != torch.bfloat16:
+        raise ValueError("gate_rows must be the contiguous [E, H] bf16 gate")
+    _lib.call(
+        "glm52_decode_norm_logits", _lib.ptr(x), x.stride(0), _lib.ptr(r), r.stride(0),
+        _lib.ptr(w_norm), _lib.ptr(h1), h1.stride(0), _lib.ptr(y), y.stride(0),
+        _lib.ptr(gate_rows), gate_rows.stride(0), _lib.ptr(logits), logits.stride(0), T, H, E,
+        float(eps), _lib.stream(),
+    )
+
+
+def route_gateup_shared_into(logits, cfg, topw, topi, sorted_token_ids, expert_ids,
+                             num_tokens_post_padded, a, w13, act, a_shared, w13_shared, act_shared):
+    """Decode (T <= 4): `topk_only` -> `moe_align_block_size` (block size 16) ->
+    `launch_gateup(fused=True)` for the routed experts and the shared expert, in one launch
+    that derives the routing from the logits (no grid-wide wait).  Writes topw, topi and the
+    three layout tensors like `topk_align_into`, act[f] for the routed slots and act_shared."""
+    bias = cfg.get("correction_bias")
+    _lib.require_gpu(logits, topw, topi, bias, sorted_token_ids, expert_ids,
+                     num_tokens_post_padded, a, w13, act, a_shared, w13_shared, act_shared)
+    T, E = logits.shape
+    k = topi.shape[1]
+    ws = w13_shared[0] if w13_shared.dim() == 3 else w13_shared
+    for t, n in ((a, "a"), (w13, "w13"), (act, "act"), (a_shared, "a_shared"), (ws, "w13_shared"),
+                 (act_shared, "act_shared")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be bf16 and contiguous along its last dim")
+    if ws.shape != w13.shape[1:] or ws.stride(0) != w13.stride(1):
+        raise ValueError("w13_shared must have the routed experts' [2I, H] shape and row stride")
+    I = act.shape[1]
+    _lib.call(
+        "glm52_moe_gemm_route_shared", _lib.ptr(logits), logits.stride(0), _lib.ptr(bias), T, E,
+        k, float(cfg.get("scale", 2.5)), int(bool(cfg.get("NORM_PROB", True))), _lib.ptr(topw),
+        topw.stride(0), _lib.ptr(topi), topi.stride(0), _lib.ptr(sorted_token_ids),
+        _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), sorted_token_ids.numel(),
+        _lib.ptr(a), a.stride(0), _lib.ptr(w13), w13.stride(0), w13.stride(1), I, _lib.ptr(act),
+        act.stride(0), _lib.ptr(a_shared), a_shared.stride(0), _lib.ptr(ws), _lib.ptr(act_shared),
+        act_shared.stride(0), I, a.shape[1], _lib.stream(),
+    )

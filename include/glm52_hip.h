@@ -99,6 +99,37 @@ int glm52_decode_front(const void* x, int64_t stride_x, const void* res, int64_t
                        int32_t* expert_ids, int32_t* num_tokens_post_padded, int32_t* counter,
                        hipStream_t stream);
 
+/* The norm and router-logits part of glm52_decode_front (T <= 4), without the top-k and
+ * the layout: h1, y and logits, bit-identical to glm52_add_rmsnorm + glm52_router_logits.
+ * Replaces add_rmsnorm.fused_add_rmsnorm (glm52/kernels/add_rmsnorm.py:234-236) followed
+ * by norm_router.router_gemm (glm52/kernels/norm_router.py:347-349). */
+int glm52_decode_norm_logits(const void* x, int64_t stride_x, const void* res, int64_t stride_r,
+                             const void* w_norm, void* h1, int64_t stride_h, void* y,
+                             int64_t stride_y, const void* gate, int64_t stride_g, float* logits,
+                             int64_t stride_l, int T, int H, int E, float eps,
+                             hipStream_t stream);
+
+/* Decode (T <= 4): glm52_router_topk_align (block_m 16) followed by glm52_moe_gemm_shared
+ * (gated, unweighted) in one launch -- the routing is derived from the logits inside the
+ * GEMM.  Writes topw / topi and the layout (sorted_token_ids, expert_ids,
+ * num_tokens_post_padded; `capacity` slots) exactly as glm52_router_topk_align, and
+ * c[f] = bf16(silu(a[f / topk] . w[e, n]) * (a[f / topk] . w[e, gate_up_offset + n])) for
+ * the routed slots, c_shared[t] likewise with w_shared for tokens t < T.  Replaces
+ * norm_router.topk_only (glm52/kernels/norm_router.py:352-354) ->
+ * reference.moe_align_block_size (glm52/reference.py:85-128) ->
+ * moe_gateup.launch_gateup(fused=True) (glm52/kernels/moe_gateup.py:199-248) for the routed
+ * and the shared expert (glm52/bench/bench_layer.py:470-480). */
+int glm52_moe_gemm_route_shared(const float* logits, int64_t stride_l, const float* bias, int T,
+                                int E, int topk, float scale, int norm_prob, float* topw,
+                                int64_t stride_w, int32_t* topi, int64_t stride_i,
+                                int32_t* sorted_token_ids, int32_t* expert_ids,
+                                int32_t* num_tokens_post_padded, int capacity, const void* a,
+                                int64_t stride_am, const void* w, int64_t stride_we,
+                                int64_t stride_wn, int gate_up_offset, void* c, int64_t stride_cm,
+                                const void* a_shared, int64_t stride_as, const void* w_shared,
+                                void* c_shared, int64_t stride_cs, int n_out, int k,
+                                hipStream_t stream);
+
 /* Grouped expert GEMM on bf16 MFMA.  Replaces moe_gateup.launch_gateup
  * (glm52/kernels/moe_gateup.py:199-248; gated = fused SwiGLU, gate_up_offset = I) and
  * moe_down_merge.launch_down with fuse_merge=False (glm52/kernels/moe_down_merge.py:427-476;
