@@ -78,6 +78,38 @@ GLM52_DEV int sload_i32(const void* base, int idx) {
   return v;
 }
 
+// Wait until at most n (wave-uniform, 0..24) of this wave's vector-memory loads are in
+// flight; the count is an immediate, so each value is one branch.
+GLM52_DEV void wait_vmcnt_at_most(int n) {
+  switch (n) {
+    case 0: GLM52_WAIT_VMCNT(0); break;
+    case 1: GLM52_WAIT_VMCNT(1); break;
+    case 2: GLM52_WAIT_VMCNT(2); break;
+    case 3: GLM52_WAIT_VMCNT(3); break;
+    case 4: GLM52_WAIT_VMCNT(4); break;
+    case 5: GLM52_WAIT_VMCNT(5); break;
+    case 6: GLM52_WAIT_VMCNT(6); break;
+    case 7: GLM52_WAIT_VMCNT(7); break;
+    case 8: GLM52_WAIT_VMCNT(8); break;
+    case 9: GLM52_WAIT_VMCNT(9); break;
+    case 10: GLM52_WAIT_VMCNT(10); break;
+    case 11: GLM52_WAIT_VMCNT(11); break;
+    case 12: GLM52_WAIT_VMCNT(12); break;
+    case 13: GLM52_WAIT_VMCNT(13); break;
+    case 14: GLM52_WAIT_VMCNT(14); break;
+    case 15: GLM52_WAIT_VMCNT(15); break;
+    case 16: GLM52_WAIT_VMCNT(16); break;
+    case 17: GLM52_WAIT_VMCNT(17); break;
+    case 18: GLM52_WAIT_VMCNT(18); break;
+    case 19: GLM52_WAIT_VMCNT(19); break;
+    case 20: GLM52_WAIT_VMCNT(20); break;
+    case 21: GLM52_WAIT_VMCNT(21); break;
+    case 22: GLM52_WAIT_VMCNT(22); break;
+    case 23: GLM52_WAIT_VMCNT(23); break;
+    default: GLM52_WAIT_VMCNT(24); break;
+  }
+}
+
 template <bool GATED, bool WEIGHTED, bool ROUTE>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
@@ -348,54 +380,52 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     *reinterpret_cast<uint2*>(dst + n0 + 4 * g) = o;
   };
 
-  // prologue: the first three stages of the first item.  In routing mode the logits are
-  // loaded first and a first item of the extra expert is issued before the routing (which
-  // waits only for the logits); a routed first item after it.
-  int n0 = 0, n1 = 0, n2 = 0;
-  auto prologue = [&]() {
-    dma_setup(d_item);
-    n0 = issue(d_s, 0);
-    dma_advance();
-    n1 = issue(d_s, 1);
-    dma_advance();
-    n2 = issue(d_s, 2);
-    dma_advance();
+  // prologue: the first three stages.  In routing mode the logits are loaded first and a
+  // first item of the extra expert has its stages issued before the routing (which waits
+  // only for the logits); the item count is known only after the routing, so the prologue
+  // stops at the end of that item (K of fewer than three stages) and goes on after it.  A
+  // routed first item is set up after the routing.
+  int nst[3] = {0, 0, 0};  // loads issued for prologue stages 0..2
+  int npro = 0;
+  auto prologue_to = [&](int upto) {  // issue prologue stages npro .. upto-1
+    while (npro < upto) {
+      nst[npro] = issue(d_s, npro);
+      if (++npro < upto) dma_advance();
+    }
   };
   const bool first_extra = (int)blockIdx.x < x_items;
   if (!ROUTE) {
     if ((int)blockIdx.x >= items) return;
-    prologue();
+    dma_setup(d_item);
+    prologue_to(3);
+    dma_advance();
   } else {
     route_load();
     if (first_extra) {
-      prologue();
+      dma_setup(d_item);
+      prologue_to(nks < 3 ? nks : 3);
       // the logits landed (this wave's; every wave's after the routing's first barrier):
       // at most the prologue's loads are still in flight
-      switch (n0 + n1 + n2) {
-        case 12: GLM52_WAIT_VMCNT(12); break;
-        case 13: GLM52_WAIT_VMCNT(13); break;
-        case 14: GLM52_WAIT_VMCNT(14); break;
-        case 15: GLM52_WAIT_VMCNT(15); break;
-        case 16: GLM52_WAIT_VMCNT(16); break;
-        case 17: GLM52_WAIT_VMCNT(17); break;
-        case 18: GLM52_WAIT_VMCNT(18); break;
-        case 19: GLM52_WAIT_VMCNT(19); break;
-        case 20: GLM52_WAIT_VMCNT(20); break;
-        case 21: GLM52_WAIT_VMCNT(21); break;
-        case 22: GLM52_WAIT_VMCNT(22); break;
-        case 23: GLM52_WAIT_VMCNT(23); break;
-        default: GLM52_WAIT_VMCNT(24); break;
-      }
+      wait_vmcnt_at_most(nst[0] + nst[1] + nst[2]);
     } else {
       GLM52_WAIT_VMCNT(0);
     }
     __syncthreads();
     route();
-    if (!first_extra) {
+    if (first_extra) {
+      dma_advance();
+      if (npro < 3) {
+        prologue_to(3);
+        dma_advance();
+      }
+    } else {
       if ((int)blockIdx.x >= items) return;
-      prologue();
+      dma_setup(d_item);
+      prologue_to(3);
+      dma_advance();
     }
   }
+  int n1 = nst[1], n2 = nst[2];
   const int total = ((items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x) * nks;
 
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -404,17 +434,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   for (int j = 0; j < total; ++j) {
     // stage j landed for this wave (stages j+1, j+2 may be in flight) and for every wave;
     // every wave is done with the buffer refilled next
-    switch (n1 + n2) {
-      case 8: GLM52_WAIT_VMCNT(8); break;
-      case 9: GLM52_WAIT_VMCNT(9); break;
-      case 10: GLM52_WAIT_VMCNT(10); break;
-      case 11: GLM52_WAIT_VMCNT(11); break;
-      case 12: GLM52_WAIT_VMCNT(12); break;
-      case 13: GLM52_WAIT_VMCNT(13); break;
-      case 14: GLM52_WAIT_VMCNT(14); break;
-      case 15: GLM52_WAIT_VMCNT(15); break;
-      default: GLM52_WAIT_VMCNT(16); break;
-    }
+    wait_vmcnt_at_most(n1 + n2);
     __syncthreads();
     n1 = n2;
     n2 = issue(d_s, (j + NSTAGE - 1) % NSTAGE);

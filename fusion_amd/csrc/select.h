@@ -134,7 +134,7 @@ GLM52_DEV void topk_weight(const float* sel_s, const int* sel_i, int topk, float
   const int lane = threadIdx.x % kWave;
   float sum = 0.f;
   for (int k = 0; k < topk; ++k) sum += sel_s[k];
-  const float denom = fmaxf(sum, 1e-20f);
+  const float denom = sum < 1e-20f ? 1e-20f : sum;  // clamp_min: a NaN sum stays NaN
   const float s = sel_s[lane];
   *w = norm_prob ? (s / denom) * scale : s * scale;
   *id = sel_i[lane];

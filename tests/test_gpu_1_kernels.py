@@ -12,8 +12,8 @@ import pytest
 import torch
 
 from fusion_amd import _lib
-from fusion_amd.dispatch import (capacity, decode_front_into, moe_align_block_size,
-                                 topk_align_into)
+from fusion_amd.dispatch import (capacity, decode_front_into, decode_norm_logits_into,
+                                 moe_align_block_size, route_gateup_shared_into, topk_align_into)
 from fusion_amd.kernels import add_rmsnorm as KN
 from fusion_amd.kernels import merge_resadd as KM
 from fusion_amd.kernels import moe_down_merge as KD
@@ -214,6 +214,120 @@ def test_decode_front_rejects_large_T(gpu):
                           torch.empty(T, 256, device=gpu), torch.empty(T, 8, device=gpu),
                           torch.empty(T, 8, dtype=torch.int32, device=gpu), 16, *bufs,
                           torch.zeros(1, dtype=torch.int32, device=gpu))
+
+
+@pytest.mark.parametrize("T", [1, 2, 3, 4])
+def test_decode_norm_logits_bitwise(gpu, T):
+    """ResAdd + RMSNorm and the router logits in one launch: the oracle's exact rule."""
+    say(f"decode norm+logits T={T}")
+    fe = front_end(T, seed=900 + T)
+    x, r, w = fe.x.to(gpu), fe.r.to(gpu), fe.w_norm.to(gpu)
+    gate_rows = fe.gate.to(gpu).contiguous()
+    y_o, h_o = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    lg_o = O.router_logits_exact(y_o, fe.wgt)
+    for rep in range(2):
+        h, y = torch.full_like(x, float("nan")), torch.full_like(x, float("nan"))
+        logits = torch.full((T, 256), float("nan"), device=gpu)
+        decode_norm_logits_into(x, r, w, h, y, gate_rows, logits)
+        torch.cuda.synchronize()
+        assert np.array_equal(u16(h), u16(h_o)) and np.array_equal(u16(y), u16(y_o))
+        assert np.array_equal(logits.cpu().numpy(), lg_o)
+
+
+def _route_logits(T, kind, rng):
+    """Router logits for the routing-launch test: random, or drawn from a few values so
+    that many keys tie, or with NaNs (their key counts as -inf)."""
+    if kind == "ties":
+        lg = rng.choice(np.array([-1.0, 0.0, 0.5, 2.0], dtype=np.float32), size=(T, 256))
+        lg[:, 200:] = 2.0  # more tied maxima than slots: lower index first
+    else:
+        lg = rng.standard_normal((T, 256)).astype(np.float32)
+    if kind == "nan":
+        lg[:, rng.choice(256, 40, replace=False)] = np.nan
+        lg[0, 3:] = np.nan  # token 0: only 3 finite keys, so NaN experts fill the top-8
+    return lg.astype(np.float32)
+
+
+ROUTE_CASES = [(1, "normal", "normal", 8, True), (2, "zero", "normal", 8, True),
+               (3, "normal", "ties", 8, True), (4, "zipf", "normal", 8, True),
+               (4, "none", "ties", 8, True), (2, "normal", "nan", 8, True),
+               (3, "normal", "normal", 6, False), (4, "zipf", "normal", 8, False)]
+
+
+@pytest.mark.parametrize("T,bias,kind,topk,norm", ROUTE_CASES)
+def test_route_gateup_shared_bitwise(gpu, T, bias, kind, topk, norm):
+    """The decode w13 launch that derives the routing itself: ids, weights and dispatch
+    layout bit for bit against the oracle's rule, and the activations bit for bit against
+    the launch that reads the oracle's layout (`moe_gemm_shared`), on two launches in a row
+    over buffers filled with garbage."""
+    say(f"route+gateup T={T} bias={bias} kind={kind} topk={topk} norm={norm}")
+    rng = np.random.default_rng(1000 * T + topk + len(kind))
+    E, H, I = 256, 1024, 256
+    lg = _route_logits(T, kind, rng)
+    if bias == "none":
+        b = None
+    elif bias == "zero":
+        b = np.zeros(E, dtype=np.float32)
+    elif bias == "zipf":
+        b = zipf_bias(E).numpy()
+    else:
+        b = (0.01 * rng.standard_normal(E)).astype(np.float32)
+    if kind == "ties" and b is not None:
+        b = rng.choice(np.array([0.0, 0.25], dtype=np.float32), size=E)
+    scale = 2.5
+    w_o, ids_o, _ = O.router_select(lg, b, topk, scale, norm)
+    rs, re_, rn = O.moe_align_block_size(ids_o, 16, E)
+    n = int(rn[0])
+    R = T * topk
+    cap = capacity(R, 16, E)
+
+    torch.manual_seed(T)
+    a = torch.randn(T, H, device=gpu).to(BF16)
+    w13 = (torch.randn(E, 2 * I, H, device=gpu) * 0.05).to(BF16)
+    w13s = (torch.randn(1, 2 * I, H, device=gpu) * 0.05).to(BF16)
+    cfg = {"correction_bias": None if b is None else torch.from_numpy(b).to(gpu),
+           "scale": scale, "NORM_PROB": norm}
+    # the same activations from the launch that reads the oracle's layout
+    sti_o = torch.full((cap,), R, dtype=torch.int32)
+    sti_o[:n] = torch.from_numpy(rs)
+    eids_o = torch.full((cap // 16,), -1, dtype=torch.int32)
+    eids_o[: n // 16] = torch.from_numpy(re_)
+    sti_o, eids_o, ntp_o = sti_o.to(gpu), eids_o.to(gpu), torch.from_numpy(rn).to(gpu)
+    act_ref = torch.empty(R, I, dtype=BF16, device=gpu)
+    act_s_ref = torch.empty(T, I, dtype=BF16, device=gpu)
+    KG.moe_gemm_shared(a, topk, w13, act_ref, None, sti_o, eids_o, ntp_o, R, I, I, True,
+                       {"BLOCK_M": 16}, a, w13s, act_s_ref)
+    logits = torch.from_numpy(lg).to(gpu)
+    for rep in range(2):
+        topw = torch.full((T, topk), float("nan"), device=gpu)
+        topi = torch.full((T, topk), -7, dtype=torch.int32, device=gpu)
+        sti = torch.full((cap,), -7, dtype=torch.int32, device=gpu)
+        eids = torch.full((cap // 16,), -7, dtype=torch.int32, device=gpu)
+        ntp = torch.full((1,), -7, dtype=torch.int32, device=gpu)
+        act = torch.full((R, I), float("nan"), dtype=BF16, device=gpu)
+        act_s = torch.full((T, I), float("nan"), dtype=BF16, device=gpu)
+        route_gateup_shared_into(logits, cfg, topw, topi, sti, eids, ntp, a, w13, act, a, w13s,
+                                 act_s)
+        torch.cuda.synchronize()
+        assert np.array_equal(topi.cpu().numpy(), ids_o)
+        np.testing.assert_array_equal(topw.cpu().numpy(), w_o)  # NaN where the oracle has NaN
+        assert int(ntp.item()) == n
+        s_, e_ = sti.cpu().numpy(), eids.cpu().numpy()
+        assert np.array_equal(s_[:n], rs) and np.array_equal(e_[: n // 16], re_)
+        assert (s_[n:] == R).all() and (e_[n // 16:] == -1).all()
+        assert torch.equal(act, act_ref) and torch.equal(act_s, act_s_ref)
+
+
+def test_route_gateup_shared_rejects_bad_shapes(gpu):
+    T, E, H, I = 5, 256, 512, 64
+    z = lambda *s, dt=torch.float32: torch.zeros(*s, dtype=dt, device=gpu)  # noqa: E731
+    a, w13 = z(T, H, dt=BF16), z(E, 2 * I, H, dt=BF16)
+    cap = capacity(T * 8, 16, E)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        route_gateup_shared_into(z(T, E), {"correction_bias": z(E)}, z(T, 8),
+                                 z(T, 8, dt=torch.int32), z(cap, dt=torch.int32),
+                                 z(cap // 16, dt=torch.int32), z(1, dt=torch.int32), a, w13,
+                                 z(T * 8, I, dt=BF16), a, w13[:1], z(T, I, dt=BF16))
 
 
 # ------------------------------------------------------------------ dispatch layout

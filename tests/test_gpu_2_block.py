@@ -78,7 +78,8 @@ def rows_reference(y, h, ids, tw, W, rows):
     return torch.stack(exact), torch.stack(faithful)
 
 
-CONFIGS = [(1, "normal"), (32, "normal"), (256, "normal"), (2048, "normal"), (8192, "zipf")]
+CONFIGS = [(1, "normal"), (4, "zipf"), (16, "normal"), (32, "normal"), (256, "normal"),
+           (2048, "normal"), (8192, "zipf")]
 
 
 @pytest.mark.parametrize("T,bias", CONFIGS)
