@@ -8,11 +8,14 @@ batch of T synthetic tokens, with the real 256-expert weight set (19.3 GB) resid
 The headline `value` is microseconds per block at T = 1 (configuration 1); T = 256 and
 8192 are reported under `per_T`.  Timing follows the reference's `bench_chain`
 (`glm52/common.py:73-122`): one cache flush (1 GiB, larger than the 256 MB Infinity
-Cache) before every step, never inside it, and HIP events around the step; decode
-steps replay a captured HIP graph.  The dominant kernel (routed w13 + SwiGLU) is also
-timed alone with events on its stream, for the `roofline` object.  The CPU baseline is
-the oracle's restatement of `glm52/reference.py`'s path (fp32 router, per-expert bf16
-`moe_mlp`, fp32 shared expert) on this host's cores at T = 1.
+Cache) before every step, never inside it, HIP events around the step, eager launches;
+decode sizes also report the replay of a captured HIP graph (`graph_us`).  The dominant kernel -- the block's w13 + SwiGLU
+launch, which at T <= 4 also derives the routing and runs the shared expert -- is also
+timed alone with events on its stream, for the `roofline` object; its HBM traffic comes
+from two `rocprofv3 --pmc` runs of a child process (`--pmc-child`), scaled by a plain
+copy of known size.  The CPU baseline is the oracle's restatement of
+`glm52/reference.py`'s path (fp32 router, per-expert bf16 `moe_mlp`, fp32 shared expert)
+on this host's cores at T = 1.
 """
 
 from __future__ import annotations
@@ -44,6 +47,11 @@ def parse():
     ap.add_argument("--json-out", default="")
     ap.add_argument("--calibrate", action="store_true",
                     help="only measure the read-bandwidth ceiling (glm52_stream_read) and exit")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 --pmc child runs behind roofline.traffic")
+    ap.add_argument("--pmc-child", action="store_true",
+                    help="(internal) the process profiled for roofline.traffic: three 256 MiB "
+                         "copies, then the block's w13 launch at the first --tokens value")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run a plain 256 MiB device copy three times: the known-size "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -65,7 +73,6 @@ def main() -> int:
 
     from fusion_amd import roofline as RL
     from fusion_amd.block import MoEBlock
-    from fusion_amd.kernels.moe_gateup import moe_gemm
     from fusion_amd.problem import expert_weights, front_end
 
     dev = torch.device("cuda:0")
@@ -73,7 +80,7 @@ def main() -> int:
     if args.calibrate:
         print(json.dumps({"calibration": calibrate(dev)}), flush=True)
         return 0
-    if args.copy_probe:
+    if args.copy_probe or args.pmc_child:
         src = torch.ones(2 ** 26, dtype=torch.int32, device=dev)  # 256 MiB
         dst = torch.empty_like(src)
         for _ in range(3):
@@ -86,6 +93,20 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"weights ready in {time.time() - t0:.1f}s")
     flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)  # 1 GiB
+    if args.pmc_child:
+        T = int(args.tokens.split(",")[0])
+        fe = front_end(T, bias="zipf" if T == 8192 else "normal")
+        x, r = fe.x.to(dev), fe.r.to(dev)
+        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), W.w13, W.w2,
+                       W.w13s, W.w2s)
+        blk(x, r)
+        torch.cuda.synchronize()
+        for _ in range(PMC_LAUNCHES):
+            flush_buf.zero_()
+            blk.w13_step()
+        torch.cuda.synchronize()
+        log(f"pmc child: T={T}, {PMC_LAUNCHES} w13 launches")
+        return 0
 
     def flush():
         flush_buf.zero_()
@@ -120,26 +141,18 @@ def main() -> int:
         blk(x, r)
         torch.cuda.synchronize()
         n_e = int(torch.unique(blk.topi).numel())
-        use_graph = (not args.no_graph) and T <= 256
-        if use_graph:
+        # the headline times eager launches, as the reference's bench_chain does; decode
+        # sizes also time a captured HIP graph of the same chain (reported, not headline:
+        # on this ROCm its replay adds launch gaps between the nodes)
+        ms, wall = timed(lambda: blk(x, r), args.steps, args.warmup)
+        graph_ms = None
+        if (not args.no_graph) and T <= 256:
             blk.capture(x, r)
-            step = blk.replay
-        else:
-            step = lambda: blk(x, r)  # noqa: E731
-        ms, wall = timed(step, args.steps, args.warmup)
-        eager_ms = None
-        if use_graph:
-            eager_ms, _ = timed(lambda: blk(x, r), args.steps, args.warmup)
+            graph_ms, _ = timed(blk.replay, args.steps, args.warmup)
 
-        # dominant kernel alone: routed w13 + SwiGLU, events on its stream
-        R = T * 8
-
-        def w13():
-            moe_gemm(blk.y, 8, blk.w13, blk.act, None, blk.sti, blk.eids, blk.ntp, R, blk.I,
-                     blk.I, True, blk.cfg_r)
-
-        k_ms, _ = timed(w13, args.steps, 2)
-        kc = RL.kernel("w13", T, n_e)
+        # dominant kernel alone: the block's w13 + SwiGLU launch, events on its stream
+        k_ms, _ = timed(blk.w13_step, args.steps, 2)
+        kc = RL.w13_launch(T, n_e, blk.shared_fused, blk.front_fused)
         k_us = statistics.mean(k_ms) * 1e3
         roof_us = RL.block_roofline_us(T, n_e)
         med_us = statistics.median(ms) * 1e3
@@ -147,8 +160,7 @@ def main() -> int:
             "us_per_block": round(med_us, 2),
             "us_mean": round(statistics.mean(ms) * 1e3, 2),
             "us_min": round(min(ms) * 1e3, 2),
-            "graph": use_graph,
-            "eager_us": round(statistics.median(eager_ms) * 1e3, 2) if eager_ms else None,
+            "graph_us": round(statistics.median(graph_ms) * 1e3, 2) if graph_ms else None,
             "wall_us_per_step_incl_flush": round(wall / args.steps * 1e6, 1),
             "distinct_experts": n_e,
             "block_roofline_us": round(roof_us, 1),
@@ -156,26 +168,34 @@ def main() -> int:
             "w13_us": round(k_us, 2),
             "w13_GBps": round(kc.bytes / (k_us * 1e-6) / 1e9, 1),
             "w13_TFLOPs": round(kc.flops / (k_us * 1e-6) / 1e12, 1),
+            "w13_launch": w13_kernel_name(blk),
             "block_m": blk.bm,
             "bias": bias,
         }
         per_T[str(T)] = rec
         log(f"T={T}: {rec}")
         if headline is None:
-            headline = (T, rec, kc, k_us, n_e)
+            headline = (T, rec, kc, k_us, n_e, w13_kernel_name(blk))
         del blk, x, r
         torch.cuda.empty_cache()
 
-    T, rec, kc, k_us, n_e = headline
+    T, rec, kc, k_us, n_e, kname = headline
     achieved = kc.bytes / (k_us * 1e-6) / 1e9
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
-            "frac": round(achieved / 8000.0, 4), "traffic": None,
-            "kernel": "moe_gemm_stream_kernel<gated> (routed w13 + SwiGLU)",
+            "frac": round(achieved / 8000.0, 4), "traffic": None, "kernel": kname,
             "algorithmic_bytes": int(kc.bytes), "avg_us": round(k_us, 2)}
-
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, tokens[0], args.cpu_seconds)
+    del W, flush_buf
+    torch.cuda.empty_cache()
+    if not args.no_traffic:
+        tr = hbm_traffic(T)
+        if tr is not None:
+            roof["traffic"] = tr["bytes"]
+            roof["traffic_over_algorithmic"] = round(tr["bytes"] / kc.bytes, 4)
+            roof["traffic_detail"] = tr
+
 
     line = {
         "metric": METRIC, "value": rec["us_per_block"], "unit": "us", "n_gpus": 1,
@@ -184,7 +204,7 @@ def main() -> int:
         "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, random init)",
         "config": {"workload": f"config1: full GLM-5.2 MoE FFN block, decode T={T}", "T": T,
                    "experts": 256, "shared_experts": 1, "topk": 8, "H": 6144, "I": 2048,
-                   "weights_GB": 19.33, "graph_replay": rec["graph"]},
+                   "weights_GB": 19.33, "launch": "eager (torch current stream)"},
         "roofline": roof,
         "cpu_baseline": cpu,
         "per_T": per_T,
@@ -194,6 +214,75 @@ def main() -> int:
     if args.json_out:
         Path(args.json_out).write_text(s + "\n")
     return 0
+
+
+PMC_LAUNCHES = 3
+COPY_KIB = 262144  # the child's plain copies: 256 MiB read and 256 MiB written each
+
+
+def w13_kernel_name(blk) -> str:
+    """The kernel behind `MoEBlock.w13_step` (as the profiler names it)."""
+    if blk.front_fused:
+        return ("moe_gemm_runs_kernel<true, false, true> (routing + routed and shared "
+                "w13 + SwiGLU)")
+    if blk.shared_fused:
+        return "moe_gemm_runs_kernel<true, false, false> (routed and shared w13 + SwiGLU)"
+    return f"moe_gemm_w512_kernel<{blk.bm}, true, false> (routed w13 + SwiGLU)"
+
+
+def hbm_traffic(T: int, timeout_s: float = 240.0) -> dict | None:
+    """HBM bytes per launch of the block's w13 launch at T tokens: two `rocprofv3 --pmc`
+    runs of a child process (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch), each counter
+    scaled by what it reads for the child's plain 256 MiB device copies.  None if the
+    profiler is missing or a run fails."""
+    import csv
+    import shutil
+    import signal
+    import subprocess
+    import tempfile
+
+    exe = shutil.which("rocprofv3")
+    if exe is None:
+        log("traffic: rocprofv3 not found")
+        return None
+    got = {}
+    for ctr in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="pmc_")
+        cmd = [exe, "--pmc", ctr, "--output-format", "csv", "-d", d, "-o", "run", "--",
+               sys.executable, str(ROOT / "bench.py"), "--pmc-child", "--tokens", str(T)]
+        log(f"traffic: {ctr} pass")
+        proc = subprocess.Popen(cmd, stdout=subprocess.DEVNULL, stderr=subprocess.PIPE,
+                                start_new_session=True, cwd=str(ROOT))
+        try:
+            _, err = proc.communicate(timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            os.killpg(proc.pid, signal.SIGKILL)
+            proc.wait()
+            log(f"traffic: {ctr} pass timed out")
+            return None
+        files = list(Path(d).rglob("*counter_collection.csv"))
+        if not files:
+            log(f"traffic: {ctr} pass gave no counters (rc {proc.returncode}): "
+                f"{err.decode(errors='replace')[-400:]}")
+            return None
+        rows = sorted(csv.DictReader(open(files[0])), key=lambda r: int(r["Dispatch_Id"]))
+        rows = [r for r in rows if r["Counter_Name"] == ctr]
+        copies = sorted((float(r["Counter_Value"]) for r in rows
+                         if "copyBuffer" in r["Kernel_Name"]), reverse=True)[:3]
+        if len(copies) < 3 or not rows:
+            log(f"traffic: {ctr} pass: copy dispatches not found")
+            return None
+        name = rows[-1]["Kernel_Name"]
+        vals = [float(r["Counter_Value"]) for r in rows if r["Kernel_Name"] == name][-PMC_LAUNCHES:]
+        scale = COPY_KIB / statistics.mean(copies)
+        got[ctr] = {"kib_raw": round(statistics.mean(vals), 1), "scale": round(scale, 4),
+                    "kernel": name.replace("void ", "").replace("(anonymous namespace)::", "")
+                    .split("(")[0]}
+        shutil.rmtree(d, ignore_errors=True)
+    f, w = got["FETCH_SIZE"], got["WRITE_SIZE"]
+    nbytes = (f["kib_raw"] * f["scale"] + w["kib_raw"] * w["scale"]) * 1024
+    return {"bytes": int(nbytes), "fetch_kib": f["kib_raw"], "fetch_scale": f["scale"],
+            "write_kib": w["kib_raw"], "write_scale": w["scale"], "kernel": f["kernel"]}
 
 
 def calibrate(dev) -> list:

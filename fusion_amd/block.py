@@ -141,8 +141,10 @@ class MoEBlock:
             KR.router(self.y, self.wgt, self.logits, self.topw, self.topi, self.cfg_topk)
             moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp)
 
-    def experts(self):
-        T, H, I, R = self.T, self.H, self.I, self.T * self.topk
+    def w13_step(self):
+        """Steps 5 and 6 (at T <= 4 also 3 and 4): one launch when the shared expert runs
+        inside the routed launch, else the routed launch (the shared one is in w2_step)."""
+        T, I, R = self.T, self.I, self.T * self.topk
         if self.front_fused:
             route_gateup_shared_into(self.logits, self.cfg_topk, self.topw, self.topi, self.sti,
                                      self.eids, self.ntp, self.y, self.w13, self.act, self.y,
@@ -150,19 +152,27 @@ class MoEBlock:
         elif self.shared_fused:
             moe_gemm_shared(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids,
                             self.ntp, R, I, I, True, self.cfg_r, self.y, self.w13s, self.act_s)
+        else:
+            moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
+                     R, I, I, True, self.cfg_r)
+
+    def w2_step(self):
+        T, H, I, R = self.T, self.H, self.I, self.T * self.topk
         if self.shared_fused:
             moe_gemm_shared(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti,
                             self.eids, self.ntp, R, H, 0, False, self.cfg_r, self.act_s, self.w2s,
                             self.s_out)
             return
-        moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
-                 R, I, I, True, self.cfg_r)
         moe_gemm(self.y, 1, self.w13s, self.act_s, None, self.ssti, self.seids, self.sntp,
                  T, I, I, True, self.cfg_s)
         moe_gemm(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti, self.eids,
                  self.ntp, R, H, 0, False, self.cfg_r)
         moe_gemm(self.act_s, 1, self.w2s, self.s_out, None, self.ssti, self.seids, self.sntp,
                  T, H, 0, False, self.cfg_s)
+
+    def experts(self):
+        self.w13_step()
+        self.w2_step()
 
     def merge(self):
         y3 = self.ybuf.view(self.T, self.topk, self.H)

@@ -52,7 +52,7 @@ typedef __attribute__((address_space(3))) uint16_t lds_u16_t;
 GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off"
                :
-               : "s"(lds_base), "v"(gptr)
+               : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(gptr)
                : "memory");
 }
 
@@ -61,7 +61,7 @@ GLM52_DEV void dma16(const uint16_t* gptr, uint32_t lds_base) {
 GLM52_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(lds_base), "v"(voff), "s"(sbase)
+               : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(sbase)
                : "memory");
 }
 
@@ -70,7 +70,7 @@ GLM52_DEV void dma16s(const void* sbase, uint32_t voff, uint32_t lds_base) {
 GLM52_DEV void dma16s_nt(const void* sbase, uint32_t voff, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2 nt"
                :
-               : "s"(lds_base), "v"(voff), "s"(sbase)
+               : "s"(__builtin_amdgcn_readfirstlane(lds_base)), "v"(voff), "s"(sbase)
                : "memory");
 }
 

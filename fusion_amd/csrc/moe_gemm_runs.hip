@@ -78,6 +78,45 @@ GLM52_DEV int sload_i32(const void* base, int idx) {
   return v;
 }
 
+typedef int sint4_t __attribute__((ext_vector_type(4)));
+
+// Expert id eids[b] and the four slot entries sti[s .. s+3] (s a multiple of 4) in one
+// scalar round trip (b and s wave-uniform).  The loads and their wait are one asm statement, so no use of a
+// result can be scheduled before the wait.
+GLM52_DEV void sload_block(const int32_t* eids, int b, const int32_t* sti, int s, int& e,
+                           int f[4]) {
+  int ev;
+  sint4_t fv;
+  asm volatile("s_load_dword %0, %2, %3\n\ts_load_dwordx4 %1, %4, %5\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(ev), "=&s"(fv)
+               : "s"(eids), "s"(__builtin_amdgcn_readfirstlane(b * 4)), "s"(sti),
+                 "s"(__builtin_amdgcn_readfirstlane(s * 4))
+               : "memory");
+  e = ev;
+  f[0] = fv.x;
+  f[1] = fv.y;
+  f[2] = fv.z;
+  f[3] = fv.w;
+}
+
+// Four scattered fp32 entries base[idx[i]] in one scalar round trip (idx wave-uniform).
+GLM52_DEV void sload_f32x4(const float* base, const int idx[4], float v[4]) {
+  int a, b, c, d;
+  asm volatile(
+      "s_load_dword %0, %4, %5\n\ts_load_dword %1, %4, %6\n\ts_load_dword %2, %4, %7\n\t"
+      "s_load_dword %3, %4, %8\n\ts_waitcnt lgkmcnt(0)"
+      : "=&s"(a), "=&s"(b), "=&s"(c), "=&s"(d)
+      : "s"(base), "s"(__builtin_amdgcn_readfirstlane(idx[0] * 4)),
+        "s"(__builtin_amdgcn_readfirstlane(idx[1] * 4)),
+        "s"(__builtin_amdgcn_readfirstlane(idx[2] * 4)),
+        "s"(__builtin_amdgcn_readfirstlane(idx[3] * 4))
+      : "memory");
+  v[0] = __builtin_bit_cast(float, a);
+  v[1] = __builtin_bit_cast(float, b);
+  v[2] = __builtin_bit_cast(float, c);
+  v[3] = __builtin_bit_cast(float, d);
+}
+
 // Wait until at most n (wave-uniform, 0..24) of this wave's vector-memory loads are in
 // flight; the count is an immediate, so each value is one branch.
 GLM52_DEV void wait_vmcnt_at_most(int n) {
@@ -143,8 +182,22 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     const int n0 = (it % num_n) * NOC;
     const bool extra = m < xm;
     const int slot = (it / (int)gridDim.x) % NMETA;
+    // the block's expert and the wave's four slot entries: from LDS in routing mode, else
+    // in one scalar round trip
     int e = 0;
-    if (!extra) e = ROUTE ? __builtin_amdgcn_readfirstlane(rs.blk_e[m - xm]) : sload_i32(p.eids, m - xm);
+    int fr[4] = {p.num_valid, p.num_valid, p.num_valid, p.num_valid};
+    if (!extra) {
+      if constexpr (ROUTE) {
+        e = __builtin_amdgcn_readfirstlane(rs.blk_e[m - xm]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tr = wvu * 4 + i;
+          fr[i] = __builtin_amdgcn_readfirstlane(tr < rs.blk_n[m - xm] ? rs.blk_f[m - xm][tr] : p.num_valid);
+        }
+      } else {
+        sload_block(p.eids, m - xm, p.sti, (m - xm) * 16 + wvu * 4, e, fr);
+      }
+    }
     const uint16_t* wbase = extra ? p.Wx : p.W + (int64_t)e * p.swe;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -153,6 +206,8 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       dw[i] = wbase + (int64_t)grow * p.swn;
     }
     da_n = 0;
+    int fs[4];
+    bool oks[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int tr = wvu * 4 + i;  // token row of the slice; real rows fill a prefix
@@ -163,19 +218,26 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
         ok = f < p.x_rows;
         da[i] = p.Ax + (int64_t)(ok ? f : 0) * p.sax;
       } else {
-        if constexpr (ROUTE)
-          f = __builtin_amdgcn_readfirstlane(tr < rs.blk_n[m - xm] ? rs.blk_f[m - xm][tr] : p.num_valid);
-        else
-          f = sload_i32(p.sti, (m - xm) * 16 + tr);
+        f = fr[i];
         ok = f < p.num_valid;
         da[i] = p.A + (int64_t)(ok ? f / p.a_div : 0) * p.sam;
       }
       da_n += ok ? 1 : 0;
-      float w = 1.f;
-      if (WEIGHTED && !extra && ok) w = __builtin_bit_cast(float, sload_i32(p.topw, f));
-      if (lane == 0) {
-        meta_tok[slot][tr] = ok ? f : -1;
-        meta_w[slot][tr] = w;
+      fs[i] = f;
+      oks[i] = ok;
+    }
+    float w[4] = {1.f, 1.f, 1.f, 1.f};
+    if (WEIGHTED && !extra) {
+      int wi[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wi[i] = oks[i] ? fs[i] : 0;  // padding slots read entry 0
+      sload_f32x4(p.topw, wi, w);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        meta_tok[slot][wvu * 4 + i] = oks[i] ? fs[i] : -1;
+        meta_w[slot][wvu * 4 + i] = w[i];
       }
     }
   };

@@ -63,3 +63,20 @@ def block_roofline_us(T: int, n_e: float, **kw) -> float:
 
 def kernel(name: str, T: int, n_e: float) -> KernelCost:
     return next(k for k in block_kernels(T, n_e) if k.name == name)
+
+
+def w13_launch(T: int, n_e: float, shared: bool, route: bool, H: int = C.H, I: int = C.I,
+               E: int = C.E, topk: int = C.TOPK) -> KernelCost:
+    """One w13 + SwiGLU launch as the block issues it: the routed experts, plus the shared
+    expert when it runs in the same launch (weight streaming), plus, when the launch derives
+    the routing itself (T <= 4), the logits and bias it reads and the ids, weights and
+    dispatch layout it writes.  Weights count once per distinct expert; the activation rows
+    are read once."""
+    R = T * topk
+    s = 1 if shared else 0
+    rows = R + s * T
+    nbytes = T * H * 2 + (n_e + s) * 2 * I * H * 2 + rows * I * 2
+    if route:
+        cap = -(-(R + E * 15) // 16) * 16
+        nbytes += T * E * 4 + E * 4 + R * 8 + 4 * (cap + cap // 16 + 1)
+    return KernelCost("w13", 2.0 * rows * H * 2 * I, nbytes)
