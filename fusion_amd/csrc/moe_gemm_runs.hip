@@ -24,7 +24,9 @@
 // last one re-read its last stage into the free buffer.  The layout entries an item needs
 // (expert, token ids, routing weights) are read with scalar loads, which do not share the
 // vector-memory counter, so reading them never drains the weight loads in flight; the
-// epilogue takes the token ids and weights from a small LDS ring.  Staged row R keeps
+// epilogue takes the token ids and weights from a small LDS ring.  The epilogue adds no
+// barrier: the waves stash their partial sums at the item's last stage, and all four
+// reduce and store them after the next stage's barrier, a quarter of the outputs each.  Staged row R keeps
 // global 16-byte chunk c at chunk c ^ (R & 15): the 16 lanes of an operand read hit 16
 // distinct bank groups.
 //
@@ -52,7 +54,7 @@ constexpr int SROWS = 32;          // 16 W rows + 16 token rows
 constexpr int SELEM = SROWS * KS;  // elements per stage
 constexpr int RT = 4;              // routing mode: at most 4 tokens
 constexpr int RSLOT = RT * 8;      // ... and at most 32 routed ids
-constexpr int NMETA = 4;           // items whose token ids / weights are kept for the epilogue
+constexpr int NMETA = 8;           // items whose token ids / weights are kept for the epilogue
 
 struct RouteLds {
   float logits[RT][kMaxE];  // the T tokens' logits and the bias, loaded straight into LDS
@@ -152,7 +154,7 @@ GLM52_DEV void wait_vmcnt_at_most(int n) {
 template <bool GATED, bool WEIGHTED, bool ROUTE>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
-  __shared__ float red[4][4][kWave];
+  __shared__ float red[2][4][4][kWave];  // partial sums of the last two items, by wave
   __shared__ int meta_tok[NMETA][16];    // flat ids of an item's token rows
   __shared__ float meta_w[NMETA][16];    // their routing weights (weighted)
   __shared__ RouteLds rs;
@@ -405,41 +407,39 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     }
     return acc;
   };
-  auto epilogue = [&](int it, floatx4_t acc) {
+  // Epilogue, in two halves.  At an item's last stage every wave stashes its partial sums
+  // (no barrier).  After the next stage's barrier all four waves finish it together: wave
+  // w takes token columns 4 w .. 4 w + 3, a lane one (token, output) pair, adds the four
+  // waves' partials in a fixed order and stores; the 16 lanes of a token write 16
+  // consecutive outputs.  A partial for W row r and token c sits in register r % 4 of
+  // lane (r / 4) * 16 + c.
+  auto stash = [&](int par, floatx4_t acc) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[wv][i][lane] = acc[i];
-    __syncthreads();
-    if (wv != 0) return;
+    for (int i = 0; i < 4; ++i) red[par][wv][i][lane] = acc[i];
+  };
+  auto rsum = [&](int par, int row, int c) {
+    const int i = row % 4, l = (row / 4) * 16 + c;
+    return ((red[par][0][i][l] + red[par][1][i][l]) + red[par][2][i][l]) + red[par][3][i][l];
+  };
+  auto finish = [&](int it, int par) {
     const int m = it / num_n;
     const int n0 = (it % num_n) * NOC;
     const bool extra = m < xm;
     const int slot = (it / (int)gridDim.x) % NMETA;
-    const int tok = meta_tok[slot][r16];
+    const int c = wv * 4 + lane / 16;  // token column of the slice
+    const int j = lane % 16;           // output of the item
+    if (GATED && j >= 8) return;
+    const int tok = meta_tok[slot][c];
     if (tok < 0) return;
-    float v[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      v[i] = ((red[0][i][lane] + red[1][i][lane]) + red[2][i][lane]) + red[3][i][lane];
+    float v;
     if (GATED) {
-      // rows 4 g + i (g < 2) are `gate` outputs 4 g + i; their `up` rows are held by lane + 32
-      const int lu = (lane + 32) % kWave;
-      float u[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        u[i] = ((red[0][i][lu] + red[1][i][lu]) + red[2][i][lu]) + red[3][i][lu];
-      if (g >= 2) return;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = silu_mul(v[i], u[i]);
-    } else if (WEIGHTED && !extra) {
-      const float w = meta_w[slot][r16];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = v[i] * w;
+      v = silu_mul(rsum(par, j, c), rsum(par, 8 + j, c));  // `gate` row j, `up` row 8 + j
+    } else {
+      v = rsum(par, j, c);
+      if (WEIGHTED && !extra) v = v * meta_w[slot][c];
     }
     uint16_t* dst = extra ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm;
-    uint2 o;
-    o.x = pack_bf16x2(v[0], v[1]);
-    o.y = pack_bf16x2(v[2], v[3]);
-    *reinterpret_cast<uint2*>(dst + n0 + 4 * g) = o;
+    dst[n0 + j] = f32_to_bf16(v);
   };
 
   // prologue: the first three stages.  In routing mode the logits are loaded first and a
@@ -492,22 +492,33 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
   int c_item = blockIdx.x, c_s = 0;
+  int pend = -1, par = 0;  // the item whose partial sums wait in red[par ^ 1], if any
 #pragma unroll 1
   for (int j = 0; j < total; ++j) {
     // stage j landed for this wave (stages j+1, j+2 may be in flight) and for every wave;
-    // every wave is done with the buffer refilled next
+    // every wave is done with the buffer refilled next, and the stashed partials are visible
     wait_vmcnt_at_most(n1 + n2);
     __syncthreads();
     n1 = n2;
     n2 = issue(d_s, (j + NSTAGE - 1) % NSTAGE);
     dma_advance();
+    if (pend >= 0) {
+      finish(pend, par ^ 1);
+      pend = -1;
+    }
     acc = compute(j % NSTAGE, acc);
     if (++c_s == nks) {
-      epilogue(c_item, acc);
+      stash(par, acc);
+      pend = c_item;
+      par ^= 1;
       acc = floatx4_t{0.f, 0.f, 0.f, 0.f};
       c_s = 0;
       c_item += gridDim.x;
     }
+  }
+  if (pend >= 0) {
+    __syncthreads();
+    finish(pend, par ^ 1);
   }
   GLM52_WAIT_VMCNT(0);  // the re-reads past the last stage land before the workgroup ends
 }
