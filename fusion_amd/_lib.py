@@ -41,6 +41,9 @@ SIGNATURES: dict[str, list] = {
                        _I, _I, _P],
     "glm52_moe_gemm_shared": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I,
                               _P, _L, _P, _P, _L, _I, _I, _I, _I, _P],
+    "glm52_pack_w512": [_P, _L, _L, _I, _I, _I, _I, _I, _P, _P],
+    "glm52_moe_gemm_packed": [_P, _L, _I, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                              _P],
     "glm52_silu_and_mul": [_P, _L, _P, _L, _I, _I, _P],
     "glm52_moe_sum": [_P, _L, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
     "glm52_resadd": [_P, _L, _P, _L, _P, _L, _I, _I, _P],
@@ -54,6 +57,7 @@ SIGNATURES: dict[str, list] = {
 # name -> (argument types, return type) for entry points that do not return a status
 QUERIES: dict[str, tuple[list, type]] = {
     "glm52_router_workspace_bytes": ([_I, _I, _I], c_int64),
+    "glm52_packed_w512_bytes": ([_I, _I, _I, _I], c_int64),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported argument combination"}

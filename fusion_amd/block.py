@@ -19,6 +19,10 @@ the routing computed live instead of frozen, and the tail fused):
                                  moe_gemm_shared)
     9. merge + ResAdd           out = bf16(sum_k Y[t, k] + h + s)         block_merge
 
+At block sizes 64 and 128 (prefill) the four GEMMs read weights packed once in the
+constructor (`pack_w512`: every 32-k stage of a 512-row W tile as 32 KB of contiguous
+memory), which computes the same bits as reading them in place.
+
 Every buffer is allocated once in the constructor (destination passing, as the
 reference's `LayerProblem` does, `glm52/bench/bench_layer.py:316-346`); `forward` only
 launches kernels on torch's current stream and never syncs, so it can be captured in a
@@ -35,7 +39,7 @@ from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
                        moe_align_block_size_into, route_gateup_shared_into, topk_align_into)
 from .kernels import add_rmsnorm as KN
 from .kernels import norm_router as KR
-from .kernels.moe_gateup import moe_gemm, moe_gemm_shared
+from .kernels.moe_gateup import moe_gemm, moe_gemm_packed, moe_gemm_shared, pack_w512
 
 BF16 = torch.bfloat16
 
@@ -76,7 +80,8 @@ def shared_layout(T: int, block_m: int, device) -> tuple[torch.Tensor, torch.Ten
 class MoEBlock:
     def __init__(self, T: int, w_norm, wgt, bias, w13, w2, w13s, w2s, block_m: int | None = None,
                  shared_block_m: int | None = None, variant: str | None = None,
-                 eps: float = C.RMS_NORM_EPS, scale: float = C.ROUTED_SCALING_FACTOR):
+                 eps: float = C.RMS_NORM_EPS, scale: float = C.ROUTED_SCALING_FACTOR,
+                 pack: bool = True):
         _lib.require_gpu(w_norm, wgt, bias, w13, w2, w13s, w2s)
         dev = w13.device
         self.T = T
@@ -123,6 +128,15 @@ class MoEBlock:
         self.router_ws = torch.empty(max(need, 8), dtype=torch.uint8, device=dev)
         self.cfg_topk = {"correction_bias": bias, "scale": scale, "workspace": self.router_ws}
         self.graph = None
+        # prefill (block sizes 64 and 128): the GEMMs read weights packed once here, every
+        # 32-k stage of a 512-row W tile as 32 KB of contiguous memory (the same bits)
+        self.packed = (pack and variant is None and not self.shared_fused
+                       and self.bm in (64, 128) and self.sbm in (64, 128))
+        if self.packed:
+            self.w13_p = pack_w512(w13, self.I, self.I, True)
+            self.w2_p = pack_w512(w2, self.H, 0, False)
+            self.w13s_p = pack_w512(self.w13s, self.I, self.I, True)
+            self.w2s_p = pack_w512(self.w2s, self.H, 0, False)
 
     # ---- the chain -------------------------------------------------------------------
     def front_end(self, x, r):
@@ -152,6 +166,9 @@ class MoEBlock:
         elif self.shared_fused:
             moe_gemm_shared(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids,
                             self.ntp, R, I, I, True, self.cfg_r, self.y, self.w13s, self.act_s)
+        elif self.packed:
+            moe_gemm_packed(self.y, self.topk, self.w13_p, self.act, None, self.sti, self.eids,
+                            self.ntp, R, I, True, self.cfg_r)
         else:
             moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
                      R, I, I, True, self.cfg_r)
@@ -162,6 +179,14 @@ class MoEBlock:
             moe_gemm_shared(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti,
                             self.eids, self.ntp, R, H, 0, False, self.cfg_r, self.act_s, self.w2s,
                             self.s_out)
+            return
+        if self.packed:
+            moe_gemm_packed(self.y, 1, self.w13s_p, self.act_s, None, self.ssti, self.seids,
+                            self.sntp, T, I, True, self.cfg_s)
+            moe_gemm_packed(self.act, 1, self.w2_p, self.ybuf, self.topw.view(-1), self.sti,
+                            self.eids, self.ntp, R, H, False, self.cfg_r)
+            moe_gemm_packed(self.act_s, 1, self.w2s_p, self.s_out, None, self.ssti, self.seids,
+                            self.sntp, T, H, False, self.cfg_s)
             return
         moe_gemm(self.y, 1, self.w13s, self.act_s, None, self.ssti, self.seids, self.sntp,
                  T, I, I, True, self.cfg_s)

@@ -128,6 +128,9 @@ struct GemmArgs {
   int32_t* r_eids;
   int32_t* r_ntp;
   int r_capacity;
+  // 512-row tile mapping: W packed per (expert, tile, 32-k stage) in the order the tile's
+  // loads fill LDS (glm52_pack_w512); null: W is read in place
+  const uint16_t* Wp;
 };
 
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
@@ -137,6 +140,12 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 // The 512-row W tile mapping (moe_gemm_wide.hip): GLM52_EUNSUPPORTED for a block size or
 // shape it has no instance for.
 int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st);
+
+// Packs W for launch_wide512 (GemmArgs::Wp): E experts, n_out outputs (gated: the `gate`
+// rows n and the `up` rows gate_up_offset + n), K = k.  Returns the bytes written, or a
+// negative error for a shape the 512-row mapping has no instance for (out = null: size only).
+int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_out, int k,
+                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st);
 
 // The decode mapping that streams W as contiguous 1 KB row runs (moe_gemm_runs.hip): block
 // size 16; an optional extra expert (x_rows > 0) as in the stream mapping; `route`: the

@@ -429,6 +429,57 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
                   : launch_tiled_bm<false, false>(g, capacity, stream);
 }
 
+// Packed weights for the 512-row tile mapping (prefill, block_m 64 or 128).  The mapping
+// reads every 32-k stage of a 512-row W tile as 512 runs of 64 bytes, one per row, which
+// the HBM serves far below its streaming rate; packed, a stage is 32 KB of contiguous
+// memory in exactly the order its loads fill LDS.  Same values, same arithmetic: the
+// packed launch computes the same bits as glm52_moe_gemm on the unpacked weights.
+extern "C" int64_t glm52_packed_w512_bytes(int num_experts, int n_out, int k, int gated) {
+  return pack_wide512(nullptr, 0, 0, num_experts, n_out, k, 0, gated != 0, nullptr, nullptr);
+}
+
+extern "C" int glm52_pack_w512(const void* w, int64_t stride_we, int64_t stride_wn,
+                               int num_experts, int n_out, int k, int gate_up_offset, int gated,
+                               void* packed, hipStream_t stream) {
+  if (!w || !packed || !al16(w) || !al16(packed) || (stride_we % 8) || (stride_wn % 8) ||
+      stride_wn < k)
+    return GLM52_EINVAL;
+  if (gated && gate_up_offset < n_out) return GLM52_EINVAL;
+  const int64_t rc = pack_wide512(static_cast<const uint16_t*>(w), stride_we, stride_wn,
+                                  num_experts, n_out, k, gate_up_offset, gated != 0,
+                                  static_cast<uint16_t*>(packed), stream);
+  if (rc == GLM52_EUNSUPPORTED) return GLM52_EUNSUPPORTED;
+  return rc < 0 ? (int)(-rc) : GLM52_OK;
+}
+
+extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row_div,
+                                     const void* w_packed, void* c, int64_t stride_cm,
+                                     const float* topk_weights,
+                                     const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                                     const int32_t* num_tokens_post_padded, int capacity,
+                                     int block_m, int num_valid_tokens, int n_out, int k,
+                                     int gated, hipStream_t stream) {
+  if (!a || !w_packed || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
+    return GLM52_EINVAL;
+  if ((block_m != 64 && block_m != 128) || capacity < 0 || (capacity % block_m) != 0)
+    return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 || (k % 64) != 0 ||
+      a_row_div <= 0)
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w_packed) || (stride_am % 8) || !al16(c) || (stride_cm % 8))
+    return GLM52_EINVAL;
+  if (capacity == 0) return GLM52_OK;
+  const int ab = a_bytes(num_valid_tokens, a_row_div, stride_am, k);
+  if (ab < 0 || ab >= 0x7ffffff0) return GLM52_EUNSUPPORTED;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
+             static_cast<const uint16_t*>(w_packed), 0, 0, gated ? n_out : 0,
+             static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
+             nullptr, 0, nullptr, nullptr, 0, 0, ab, 0};
+  g.Wp = static_cast<const uint16_t*>(w_packed);
+  return launch_wide512(g, capacity, gated != 0, topk_weights != nullptr, stream);
+}
+
 // The routed grouped GEMM and the shared expert's GEMM in one weight-streaming launch
 // (decode): the shared expert is an extra expert whose rows are the tokens 0 .. T - 1 of
 // its own input (no routing weight), written to its own output.  Same operand rules as

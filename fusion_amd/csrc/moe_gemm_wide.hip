@@ -332,7 +332,22 @@ namespace {
 // W row (inside its 32-row group) held at LDS row p.
 GLM52_DEV int phi32(int p) { return ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); }
 
-template <int MT, bool GATED, bool WEIGHTED>
+// Packed W (PACKED): for expert e and output tile pid_n the tile's stages follow each other,
+// 32 KB each ((e * num_n + pid_n) * nk + kt), and inside a stage the 1 KB of wave w's load
+// instruction i sits at (w * 8 + i) * 1 KB, lane l's 16 bytes at l * 16: exactly what the
+// instruction writes to LDS, so every load reads 1 KB of contiguous memory.
+constexpr int kPackStage = 32768;  // bytes of one packed stage (512 rows x 32 k x 2 B)
+
+// W row (relative to the tile's first `gate` row, or to n0) and k chunk of packed lane l of
+// load instruction i of wave w: the row and chunk the unpacked loads of that slot fetch.
+GLM52_DEV int w512_row(bool gated, int gu_rel, int w, int i, int l) {
+  const int f = i >> 1;
+  const int base = gated ? (f >= 2 ? gu_rel : 0) + w * 64 + (f & 1) * 32 : w * 128 + f * 32;
+  return base + (i & 1) * 8 + phi32(l >> 2);
+}
+GLM52_DEV int w512_chunk(int l) { return (l & 3) ^ (((l >> 2) >> 2) & 3); }
+
+template <int MT, bool GATED, bool WEIGHTED, bool PACKED>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   constexpr int NTW = 512;         // W rows per tile
   constexpr int BKS = 32;          // k per stage
@@ -399,14 +414,17 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     // W load instruction i of the wave fills slab rows i*16 .. +15: W rows
     // wrow(i) + phi32(lane / 4) (wrow(i) wave-uniform), 16 bytes at logical chunk dc each;
     // the lane's byte offsets inside W[e] (< 2^32: an expert's W is far smaller)
-    const uint16_t* wexp = p.W + (int64_t)e * p.swe;
+    const uint16_t* wexp = PACKED ? p.Wp + (int64_t)(e * num_n + pid_n) * nk * (kPackStage / 2)
+                                  : p.W + (int64_t)e * p.swe;
     uint32_t wvoff[WI];
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
-      const int f = i >> 1;
-      const int base = GATED ? (f >= 2 ? p.gu_off : 0) + n0 + wv * 64 + (f & 1) * 32
-                             : n0 + wv * 128 + f * 32;
-      wvoff[i] = (uint32_t)(((int64_t)(base + (i & 1) * 8 + phi32(dr)) * p.swn + dc * 8) * 2);
+      if (PACKED) {
+        wvoff[i] = (uint32_t)((wv * WI + i) * 1024 + lane * 16);
+      } else {
+        const int row = n0 + w512_row(GATED, p.gu_off, wv, i, lane);
+        wvoff[i] = (uint32_t)(((int64_t)row * p.swn + dc * 8) * 2);
+      }
     }
     uint32_t avoff[AI];  // byte offsets of the lane's token rows in A (< 2^31, checked)
 #pragma unroll
@@ -421,7 +439,8 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       const int kc = min(kt, nk - 1) * BKS;
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
-        dma16s(wexp + kc, wvoff[i], sb + (uint32_t)((wvu * 128 + i * RPI) * BKS * 2));
+        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * (kPackStage / 2) : wexp + kc;
+        dma16s(src, wvoff[i], sb + (uint32_t)((wvu * 128 + i * RPI) * BKS * 2));
       } else {
         const int j = i - WI;
         dma16s(p.A + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
@@ -546,7 +565,10 @@ int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
   const int items_max = (capacity / MT) * (a.n_out / NO);
   int grid = items_max < 256 ? items_max : 256;
   grid = ((grid + 7) / 8) * 8;
-  moe_gemm_w512_kernel<MT, GATED, WEIGHTED><<<grid, 256, 0, st>>>(a);
+  if (a.Wp)
+    moe_gemm_w512_kernel<MT, GATED, WEIGHTED, true><<<grid, 256, 0, st>>>(a);
+  else
+    moe_gemm_w512_kernel<MT, GATED, WEIGHTED, false><<<grid, 256, 0, st>>>(a);
   GLM52_RETURN_LAUNCH();
 }
 
@@ -559,11 +581,52 @@ int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
   }
 }
 
+// One 16-byte chunk of the packed layout per thread and step: destination chunk d is lane
+// d % 64 of load instruction (d / 64) % 32 of stage (d / 2048) % nk of tile d / (2048 nk).
+template <bool GATED>
+__global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restrict__ w,
+                                                        int64_t swe, int64_t swn, int gu_off,
+                                                        int num_n, int nk, int64_t chunks,
+                                                        uint16_t* __restrict__ out) {
+  constexpr int NO = GATED ? 256 : 512;
+  for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < chunks;
+       d += (int64_t)gridDim.x * 256) {
+    const int l = (int)(d % 64);
+    const int slot = (int)((d / 64) % 32);
+    const int64_t rest = d / 2048;
+    const int kt = (int)(rest % nk);
+    const int64_t tile = rest / nk;
+    const int pid_n = (int)(tile % num_n);
+    const int64_t e = tile / num_n;
+    const int row = pid_n * NO + w512_row(GATED, gu_off, slot / 8, slot % 8, l);
+    const uint16_t* src = w + e * swe + (int64_t)row * swn + kt * 32 + w512_chunk(l) * 8;
+    *reinterpret_cast<uint4*>(out + d * 8) = *reinterpret_cast<const uint4*>(src);
+  }
+}
+
 }  // namespace
 
 namespace glm52 {
 int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, hipStream_t st) {
   if (gated) return weighted ? launch_w512_bm<true, true>(a, capacity, st) : launch_w512_bm<true, false>(a, capacity, st);
   return weighted ? launch_w512_bm<false, true>(a, capacity, st) : launch_w512_bm<false, false>(a, capacity, st);
+}
+
+int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_out, int k,
+                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st) {
+  const int NO = gated ? 256 : 512;
+  if (E <= 0 || n_out <= 0 || (n_out % NO) || k <= 0 || (k % 64)) return GLM52_EUNSUPPORTED;
+  const int num_n = n_out / NO, nk = k / 32;
+  const int64_t chunks = (int64_t)E * num_n * nk * 2048;
+  const int64_t bytes = chunks * 16;
+  if (!out) return bytes;
+  const int64_t blocks = (chunks + 255) / 256;
+  const int grid = (int)(blocks < 65536 ? blocks : 65536);
+  if (gated)
+    pack_w512_kernel<true><<<grid, 256, 0, st>>>(w, swe, swn, gate_up_offset, num_n, nk, chunks, out);
+  else
+    pack_w512_kernel<false><<<grid, 256, 0, st>>>(w, swe, swn, 0, num_n, nk, chunks, out);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? bytes : -(int64_t)err;
 }
 }  // namespace glm52

@@ -68,6 +68,45 @@ def moe_gemm(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
     )
 
 
+def pack_w512(w, n_out: int, gate_up_offset: int, gated: bool) -> torch.Tensor:
+    """The packed copy of `w` ([E, N, K] bf16, K contiguous) read by `moe_gemm_packed`: every
+    32-k stage of a 512-row W tile as 32 KB of contiguous memory (same values).  Returns a
+    flat bf16 device tensor."""
+    _lib.require_gpu(w)
+    if w.dtype != torch.bfloat16 or w.dim() != 3 or w.stride(2) != 1:
+        raise ValueError("w must be a [E, N, K] bf16 tensor with K contiguous")
+    E, _, K = w.shape
+    nbytes = _lib.query("glm52_packed_w512_bytes", E, int(n_out), K, int(gated))
+    if nbytes < 0:
+        raise ValueError(f"no 512-row tile instance for n_out={n_out}, K={K}")
+    out = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=w.device)
+    _lib.call("glm52_pack_w512", _lib.ptr(w), w.stride(0), w.stride(1), E, int(n_out), K,
+              int(gate_up_offset), int(gated), _lib.ptr(out), _lib.stream())
+    return out
+
+
+def moe_gemm_packed(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids, expert_ids,
+                    num_tokens_post_padded, num_valid_tokens, n_out, gated, cfg):
+    """`moe_gemm` (BLOCK_M 64 or 128) on weights packed by `pack_w512`: the same bits."""
+    _lib.require_gpu(a, w_packed, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                     topk_weights)
+    if a.dtype != torch.bfloat16 or w_packed.dtype != torch.bfloat16 or c.dtype != torch.bfloat16:
+        raise ValueError("grouped GEMM operands are bf16")
+    if a.stride(1) != 1 or c.stride(1) != 1:
+        raise ValueError("A rows and C rows must be contiguous")
+    if topk_weights is not None and (topk_weights.dtype != torch.float32
+                                     or not topk_weights.is_contiguous()):
+        raise ValueError("topk weights must be a contiguous fp32 tensor")
+    bm = int(cfg["BLOCK_M"])
+    cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    _lib.call(
+        "glm52_moe_gemm_packed", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w_packed),
+        _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights), _lib.ptr(sorted_token_ids),
+        _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), cap, bm, int(num_valid_tokens),
+        int(n_out), a.shape[1], int(gated), _lib.stream(),
+    )
+
+
 def moe_gemm_shared(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
                     num_tokens_post_padded, num_valid_tokens, n_out, gate_up_offset, gated, cfg,
                     a_shared, w_shared, c_shared):

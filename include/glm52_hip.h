@@ -137,7 +137,9 @@ int glm52_moe_gemm_route_shared(const float* logits, int64_t stride_l, const flo
  * W is [E, N, K] with K contiguous, C rows are indexed by the flat token id.
  * variant: 0 auto, 1 weight-streaming, 2 register-staged LDS tiles (block_m in {32, 64,
  * 128}), 3 / 4 wide 256-row W tiles fed by direct global -> LDS loads through 64-k / 32-k
- * stages (block_m in {64, 128}); auto streams at block_m 16, runs 3 at 64 and 128. */
+ * stages (block_m in {64, 128}), 5 512-row W tiles on the 32x32x16 MFMA (block_m in
+ * {64, 128}), 6 contiguous-run weight stream (block_m 16); auto runs 6 at block_m 16 and
+ * 5 at 64 and 128, falling back to 1 and 3 for shapes those have no instance for. */
 int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                    int64_t stride_we, int64_t stride_wn, int gate_up_offset, void* c,
                    int64_t stride_cm, const float* topk_weights, const int32_t* sorted_token_ids,
@@ -158,6 +160,27 @@ int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row_div, const
                           int num_valid_tokens, const void* a_shared, int64_t stride_as,
                           const void* w_shared, void* c_shared, int64_t stride_cs,
                           int shared_rows, int n_out, int k, int gated, hipStream_t stream);
+
+/* Packed weights for the prefill mapping (block_m 64 or 128): no counterpart in the
+ * reference, whose kernels read W in place.  That mapping reads each 32-k stage of a
+ * 512-row W tile as 512 runs of 64 bytes; the packed copy holds every stage as 32 KB of
+ * contiguous memory in the order the tile's loads fill LDS.  Packing is done once per
+ * weight tensor; the GEMM on the packed copy computes the same bits as glm52_moe_gemm
+ * (variant 5) on the original.
+ *   glm52_packed_w512_bytes: bytes of the packed copy of num_experts experts' W for n_out
+ *     outputs (gated: `gate` rows n and `up` rows gate_up_offset + n) and K = k; negative
+ *     if the mapping has no instance for the shape (n_out % 256 gated / 512 plain, k % 64).
+ *   glm52_pack_w512: writes that copy (w, strides, gate_up_offset as for glm52_moe_gemm).
+ *   glm52_moe_gemm_packed: glm52_moe_gemm with block_m 64 or 128 on the packed copy. */
+int64_t glm52_packed_w512_bytes(int num_experts, int n_out, int k, int gated);
+int glm52_pack_w512(const void* w, int64_t stride_we, int64_t stride_wn, int num_experts,
+                    int n_out, int k, int gate_up_offset, int gated, void* packed,
+                    hipStream_t stream);
+int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row_div, const void* w_packed,
+                          void* c, int64_t stride_cm, const float* topk_weights,
+                          const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                          const int32_t* num_tokens_post_padded, int capacity, int block_m,
+                          int num_valid_tokens, int n_out, int k, int gated, hipStream_t stream);
 
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */

@@ -459,6 +459,47 @@ def test_grouped_gemm_full_width(gpu):
         _close(y, _down_ref(act, w2, ids, tw), f"w2 {variant}")
 
 
+@pytest.mark.parametrize("bm", [64, 128])
+@pytest.mark.parametrize("T,E,H,I", [(300, 8, 512, 256), (200, 8, 6144, 2048)])
+def test_packed_w512_matches_unpacked(gpu, bm, T, E, H, I):
+    """The prefill GEMM on packed weights: the same bits as on the weights in place, for the
+    gated w13 + SwiGLU, the weighted w2 and the plain (shared-expert) w2."""
+    say(f"packed w512 bm={bm} T={T} E={E} H={H} I={I}")
+    k = 8  # every slot of the layout is routed (E >= k distinct ids per token)
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 60 + bm, gpu)
+    ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
+    cfg = {"BLOCK_M": bm, "variant": "w512"}
+    R = T * k
+    w13p = KG.pack_w512(w13g, I, I, True)
+    w2p = KG.pack_w512(w2g, H, 0, False)
+    assert w13p.numel() == w13g.numel() and w2p.numel() == w2g.numel()
+    act = torch.empty(R, I, dtype=BF16, device=gpu)
+    KG.moe_gemm(ag, k, w13g, act, None, sti, eids, ntp, R, I, I, True, cfg)
+    act_p = torch.full_like(act, float("nan"))
+    KG.moe_gemm_packed(ag, k, w13p, act_p, None, sti, eids, ntp, R, I, True, cfg)
+    twf = tw.reshape(-1).contiguous().to(gpu)
+    y = torch.empty(R, H, dtype=BF16, device=gpu)
+    KG.moe_gemm(act, 1, w2g, y, twf, sti, eids, ntp, R, H, 0, False, cfg)
+    y_p = torch.full_like(y, float("nan"))
+    KG.moe_gemm_packed(act, 1, w2p, y_p, twf, sti, eids, ntp, R, H, False, cfg)
+    y0 = torch.empty(R, H, dtype=BF16, device=gpu)
+    KG.moe_gemm(act, 1, w2g, y0, None, sti, eids, ntp, R, H, 0, False, cfg)
+    y0_p = torch.full_like(y0, float("nan"))
+    KG.moe_gemm_packed(act, 1, w2p, y0_p, None, sti, eids, ntp, R, H, False, cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(act_p, act)
+    assert torch.equal(y_p, y)
+    assert torch.equal(y0_p, y0)
+    _close(act, _gateup_ref(a, w13, ids, k, I, True), "w13 (packed path reference)")
+
+
+def test_pack_w512_rejects_unsupported_shape(gpu):
+    w = torch.zeros(2, 384, 512, dtype=BF16, device=gpu)
+    with pytest.raises(ValueError, match="no 512-row tile instance"):
+        KG.pack_w512(w, 384, 0, False)
+
+
 @pytest.mark.parametrize("T", [1, 3, 16])
 def test_moe_gemm_shared_matches_separate_launches(gpu, T):
     """Routed + shared expert in one weight-streaming launch: the same bits as the two
