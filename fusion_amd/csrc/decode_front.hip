@@ -16,9 +16,11 @@
 // wave dots its row with the staged rows.  The workgroups publish their logits, then count themselves
 // on a device-scope counter; the last one to arrive runs the top-k of every token and
 // builds the layout, then resets the counter to zero for the next launch.  The counter
-// is the only state and must be zero before the first launch.  glm52_decode_norm_logits
-// runs the kernel without that last step (no counter): the routed decode GEMM derives the
-// routing from the logits itself.
+// is the only state and must be zero before the first launch.
+//
+// glm52_decode_norm_logits computes the first two steps only (the routed decode GEMM
+// derives the routing from the logits itself) with its own mapping, norm_logits_kernel:
+// one workgroup per gate row.
 #include "select.h"
 
 using namespace glm52;
@@ -29,7 +31,6 @@ constexpr int kTmax = 4;
 constexpr int kHmax = 8192;
 constexpr int kChunks = kHmax / 8 / 256;  // 16-byte chunks per thread of one row
 
-template <bool TAIL>
 __global__ __launch_bounds__(256) void decode_front_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ wn, uint16_t* __restrict__ h_out, uint16_t* __restrict__ y_out,
@@ -148,13 +149,14 @@ __global__ __launch_bounds__(256) void decode_front_kernel(
     }
 #pragma unroll
     for (int t = 0; t < kTmax; ++t) {
-      const double s = wave_sum_f64(acc[t]);
-      if (lane == 0 && t < T) logits[(int64_t)t * sl + e] = (float)s;
+      if (t < T) {  // each reduction is 12 cross-lane moves: only the tokens that exist
+        const double s = wave_sum_f64(acc[t]);
+        if (lane == 0) logits[(int64_t)t * sl + e] = (float)s;
+      }
     }
   }
 
   // ---- 3. the last workgroup to arrive selects and builds the layout -----------------
-  if (!TAIL) return;
   __threadfence();  // publish this workgroup's logits (and h, y) device-wide
   __syncthreads();
   if (tid == 0) is_last = atomicAdd(counter, 1) == (int)gridDim.x - 1;
@@ -164,6 +166,113 @@ __global__ __launch_bounds__(256) void decode_front_kernel(
   topk_align_block(logits, sl, bv, bias != nullptr, topw, stw, topi, sti, T, E, topk, scale,
                    norm_prob, BM, capacity, sorted_ids, expert_ids, ntp_out, tsh);
   if (tid == 0) atomicExch(counter, 0);
+}
+
+// Norm and router logits only (glm52_decode_norm_logits): one workgroup per gate row, so
+// all CUs stream the gate.  Thread (wave w, lane l) owns the 16-byte chunks
+// c = w * H / 32 + l + 64 j of every token row: it adds x and r there, squares h for the
+// row's statistic, forms y there once rstd is known, and dots y with the same chunks of
+// the workgroup's gate row -- y never goes through LDS.  The statistic and the logit each
+// meet as four wave partials added in wave order.
+constexpr int kNJ = kHmax / 32 / kWave;  // chunks per thread (H <= 8192)
+
+__global__ __launch_bounds__(256) void norm_logits_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const uint16_t* __restrict__ wn, uint16_t* __restrict__ h_out, uint16_t* __restrict__ y_out,
+    int64_t sx, int64_t sr, int64_t sh_, int64_t sy, const uint16_t* __restrict__ gate,
+    int64_t sg, float* __restrict__ logits, int64_t sl, int T, int H, float eps) {
+  __shared__ double part[kTmax][4];
+  __shared__ double lpart[kTmax][4];
+  const int tid = threadIdx.x;
+  const int lane = tid % kWave;
+  const int wv = tid / kWave;
+  const int e = blockIdx.x;
+  const int qc = H / 32;  // chunks of one wave's quarter of a row
+
+  // loads, in the order they are needed: x and r of every token, the norm weight, the gate
+  uint4 xr[kTmax][kNJ][2];
+  uint4 wraw[kNJ], graw[kNJ];
+#pragma unroll
+  for (int t = 0; t < kTmax; ++t)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+      const int c = wv * qc + lane + 64 * j;
+      const bool ok = t < T && lane + 64 * j < qc;
+      xr[t][j][0] = ok ? *reinterpret_cast<const uint4*>(x + t * sx + c * 8) : make_uint4(0, 0, 0, 0);
+      xr[t][j][1] = ok ? *reinterpret_cast<const uint4*>(res + t * sr + c * 8) : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int c = wv * qc + lane + 64 * j;
+    const bool ok = lane + 64 * j < qc;
+    wraw[j] = ok ? *reinterpret_cast<const uint4*>(wn + c * 8) : make_uint4(0, 0, 0, 0);
+    graw[j] = ok ? *reinterpret_cast<const uint4*>(gate + (int64_t)e * sg + c * 8) : make_uint4(0, 0, 0, 0);
+  }
+
+  // h = bf16(x + r) and the sum of its exact squares in fp64, per token
+  uint4 hb[kTmax][kNJ];
+#pragma unroll
+  for (int t = 0; t < kTmax; ++t) {
+    if (t < T) {
+      double ss = 0.0;
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        float xf[8], rf[8], hv[8];
+        unpack8(xr[t][j][0], xf);
+        unpack8(xr[t][j][1], rf);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) xf[q] = xf[q] + rf[q];
+        hb[t][j] = pack8(xf);
+        unpack8(hb[t][j], hv);
+        if (lane + 64 * j < qc) {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) ss += (double)(hv[q] * hv[q]);
+          if (e == 0) *reinterpret_cast<uint4*>(h_out + t * sh_ + (wv * qc + lane + 64 * j) * 8) = hb[t][j];
+        }
+      }
+      ss = wave_sum_f64(ss);
+      if (lane == 0) part[t][wv] = ss;
+    }
+  }
+  __syncthreads();
+
+  // y = bf16(fp32(bf16(h * rstd)) * w) on the thread's chunks, dotted with the gate row
+  double acc[kTmax];
+#pragma unroll
+  for (int t = 0; t < kTmax; ++t) {
+    acc[t] = 0.0;
+    if (t < T) {
+      const double ssum = ((part[t][0] + part[t][1]) + part[t][2]) + part[t][3];
+      const float rstd = (float)(1.0 / sqrt(ssum / (double)H + (double)eps));
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        if (lane + 64 * j < qc) {
+          float hv[8], wf[8], gf[8], yf[8];
+          unpack8(hb[t][j], hv);
+          unpack8(wraw[j], wf);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) yf[q] = bf16_to_f32(f32_to_bf16(hv[q] * rstd)) * wf[q];
+          const uint4 yb = pack8(yf);
+          if (e == 0) *reinterpret_cast<uint4*>(y_out + t * sy + (wv * qc + lane + 64 * j) * 8) = yb;
+          unpack8(yb, yf);
+          unpack8(graw[j], gf);
+#pragma unroll
+          for (int q = 0; q < 8; ++q) acc[t] = fma((double)yf[q], (double)gf[q], acc[t]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < kTmax; ++t) {
+    if (t < T) {
+      const double s = wave_sum_f64(acc[t]);
+      if (lane == 0) lpart[t][wv] = s;
+    }
+  }
+  __syncthreads();
+  if (tid < T)
+    logits[(int64_t)tid * sl + e] =
+        (float)(((lpart[tid][0] + lpart[tid][1]) + lpart[tid][2]) + lpart[tid][3]);
 }
 
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -193,7 +302,7 @@ extern "C" int glm52_decode_front(const void* x, int64_t stride_x, const void* r
     return GLM52_EINVAL;
   const int64_t need = (int64_t)T * topk + (int64_t)E * (block_m - 1);
   if (capacity < need || (capacity % block_m)) return GLM52_EINVAL;
-  decode_front_kernel<true><<<(E + 3) / 4, 256, 0, stream>>>(
+  decode_front_kernel<<<(E + 3) / 4, 256, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res),
       static_cast<const uint16_t*>(w_norm), static_cast<uint16_t*>(h1), static_cast<uint16_t*>(y),
       stride_x, stride_r, stride_h, stride_y, static_cast<const uint16_t*>(gate), stride_g, bias,
@@ -210,18 +319,17 @@ extern "C" int glm52_decode_norm_logits(const void* x, int64_t stride_x, const v
                                         const void* gate, int64_t stride_g, float* logits,
                                         int64_t stride_l, int T, int H, int E, float eps,
                                         hipStream_t stream) {
-  if (T < 1 || T > kTmax || H <= 0 || H > kHmax || (H % 8) || E <= 0 || E > kMaxE || (E % 4))
+  if (T < 1 || T > kTmax || H <= 0 || H > kHmax || (H % 32) || E <= 0 || E > kMaxE)
     return GLM52_EINVAL;
   if (!x || !res || !w_norm || !h1 || !y || !gate || !logits) return GLM52_EINVAL;
   if (!al16(x) || !al16(res) || !al16(w_norm) || !al16(h1) || !al16(y) || !al16(gate) ||
       (stride_x % 8) || (stride_r % 8) || (stride_h % 8) || (stride_y % 8) || (stride_g % 8) ||
       stride_g < H || stride_l < E)
     return GLM52_EINVAL;
-  decode_front_kernel<false><<<(E + 3) / 4, 256, 0, stream>>>(
+  norm_logits_kernel<<<E, 256, 0, stream>>>(
       static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(res),
       static_cast<const uint16_t*>(w_norm), static_cast<uint16_t*>(h1), static_cast<uint16_t*>(y),
-      stride_x, stride_r, stride_h, stride_y, static_cast<const uint16_t*>(gate), stride_g, nullptr,
-      logits, stride_l, nullptr, 0, nullptr, 0, T, H, E, 1, eps, 1.f, 1, 16, 0, nullptr, nullptr,
-      nullptr, nullptr);
+      stride_x, stride_r, stride_h, stride_y, static_cast<const uint16_t*>(gate), stride_g,
+      logits, stride_l, T, H, eps);
   GLM52_RETURN_LAUNCH();
 }

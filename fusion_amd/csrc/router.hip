@@ -235,8 +235,10 @@ __global__ __launch_bounds__(256) void router_rows_kernel(
   }
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
-    const double s = wave_sum_f64(acc[t]);
-    if (lane == 0 && t < nt) logits[(int64_t)(t0 + t) * sl + e] = (float)s;
+    if (t < nt) {  // each reduction is 12 cross-lane moves: only the tokens that exist
+      const double s = wave_sum_f64(acc[t]);
+      if (lane == 0) logits[(int64_t)(t0 + t) * sl + e] = (float)s;
+    }
   }
 }
 
