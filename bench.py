@@ -47,6 +47,8 @@ def parse():
     ap.add_argument("--json-out", default="")
     ap.add_argument("--calibrate", action="store_true",
                     help="only measure the read-bandwidth ceiling (glm52_stream_read) and exit")
+    ap.add_argument("--no-oproj", action="store_true",
+                    help="skip the o_proj + ResAdd1 timing reported beside each T")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs behind roofline.traffic")
     ap.add_argument("--pmc-child", action="store_true",
@@ -172,6 +174,8 @@ def main() -> int:
             "block_m": blk.bm,
             "bias": bias,
         }
+        if not args.no_oproj:
+            rec["oproj"] = oproj_bench(T, timed, args.steps, args.warmup, dev)
         per_T[str(T)] = rec
         log(f"T={T}: {rec}")
         if headline is None:
@@ -283,6 +287,39 @@ def hbm_traffic(T: int, timeout_s: float = 240.0) -> dict | None:
     nbytes = (f["kib_raw"] * f["scale"] + w["kib_raw"] * w["scale"]) * 1024
     return {"bytes": int(nbytes), "fetch_kib": f["kib_raw"], "fetch_scale": f["scale"],
             "write_kib": w["kib_raw"], "write_scale": w["scale"], "kernel": f["kernel"]}
+
+
+def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
+    """o_proj + ResAdd1 (upstream of the block, not part of `value`): the fused chain of
+    `fusion_amd.kernels.oproj_resadd` on the reference's inputs for this T
+    (`glm52/bench/bench_f01_oproj_resadd.py:224-236`), timed like the block."""
+    import torch
+
+    from fusion_amd import roofline as RL
+    from fusion_amd.kernels import oproj_resadd as KO
+
+    K, N = RL.oproj_k(T), 6144
+    g = torch.Generator(device=dev).manual_seed(1234)
+    a = (torch.randn(T, K, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    b = (torch.randn(K, N, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    r = (torch.randn(T, N, device=dev, generator=g) * 0.5).to(torch.bfloat16)
+    out = torch.empty(T, N, device=dev, dtype=torch.bfloat16)
+    acc32 = torch.zeros(T, N, device=dev, dtype=torch.float32)
+    chain = KO.make_fused_chain(a, b, r, out, acc32, {"SPLIT_K": 1})
+
+    def step():
+        for fn in chain:
+            fn()
+
+    ms, _ = timed(step, steps, warmup)
+    us = statistics.median(ms) * 1e3
+    kc = RL.oproj_cost(T, K, N)
+    roof = kc.seconds() * 1e6
+    del a, b, r, out, acc32
+    return {"K": K, "us": round(us, 2), "roofline_us": round(roof, 1),
+            "roofline_frac": round(roof / us, 4), "bound": kc.bound(),
+            "GBps": round(kc.bytes / (us * 1e-6) / 1e9, 1),
+            "TFLOPs": round(kc.flops / (us * 1e-6) / 1e12, 1)}
 
 
 def calibrate(dev) -> list:

@@ -44,6 +44,10 @@ SIGNATURES: dict[str, list] = {
     "glm52_pack_w512": [_P, _L, _L, _I, _I, _I, _I, _I, _P, _P],
     "glm52_moe_gemm_packed": [_P, _L, _I, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                               _P],
+    "glm52_oproj_pack": [_P, _L, _L, _I, _I, _I, _P, _P],
+    "glm52_oproj_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L,
+                         _P],
+    "glm52_cast_add": [_P, _I, _L, _P, _L, _P, _L, _I, _I, _P],
     "glm52_silu_and_mul": [_P, _L, _P, _L, _I, _I, _P],
     "glm52_moe_sum": [_P, _L, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
     "glm52_resadd": [_P, _L, _P, _L, _P, _L, _I, _I, _P],
@@ -58,6 +62,9 @@ SIGNATURES: dict[str, list] = {
 QUERIES: dict[str, tuple[list, type]] = {
     "glm52_router_workspace_bytes": ([_I, _I, _I], c_int64),
     "glm52_packed_w512_bytes": ([_I, _I, _I, _I], c_int64),
+    "glm52_oproj_workspace_bytes": ([_I, _I, _I], c_int64),
+    "glm52_oproj_packed_bytes": ([_I, _I], c_int64),
+    "glm52_oproj_splits": ([_I, _I, _I], c_int),
 }
 
 ERRORS = {-1: "invalid argument", -2: "unsupported argument combination"}

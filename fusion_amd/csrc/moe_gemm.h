@@ -131,6 +131,13 @@ struct GemmArgs {
   // 512-row tile mapping: W packed per (expert, tile, 32-k stage) in the order the tile's
   // loads fill LDS (glm52_pack_w512); null: W is read in place
   const uint16_t* Wp;
+  // 512-row tile mapping, plain and unweighted only: epilogue 0 = bf16(acc); 1 =
+  // bf16(acc + R); 2 = C32 += acc (+ R if R); 3 = C32 = acc (fp32 partial sums): the
+  // dense GEMM + residual of o_proj
+  int epi;
+  const uint16_t* R;
+  int64_t srm;
+  float* C32;
 };
 
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
@@ -145,7 +152,8 @@ int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, h
 // rows n and the `up` rows gate_up_offset + n), K = k.  Returns the bytes written, or a
 // negative error for a shape the 512-row mapping has no instance for (out = null: size only).
 int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_out, int k,
-                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st);
+                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st,
+                     int64_t swk = 1);
 
 // The decode mapping that streams W as contiguous 1 KB row runs (moe_gemm_runs.hip): block
 // size 16; an optional extra expert (x_rows > 0) as in the stream mapping; `route`: the

@@ -347,7 +347,7 @@ GLM52_DEV int w512_row(bool gated, int gu_rel, int w, int i, int l) {
 }
 GLM52_DEV int w512_chunk(int l) { return (l & 3) ^ (((l >> 2) >> 2) & 3); }
 
-template <int MT, bool GATED, bool WEIGHTED, bool PACKED>
+template <int MT, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   constexpr int NTW = 512;         // W rows per tile
   constexpr int BKS = 32;          // k per stage
@@ -522,7 +522,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       for (int t = 0; t < NV; ++t) {
         const int tok = p.sti[row0 + t * 32 + l32];
         if (tok >= p.num_valid) continue;
-        uint16_t* crow = p.C + (int64_t)tok * p.scm;
+        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;
         if (GATED) {
 #pragma unroll
           for (int fp = 0; fp < 2; ++fp) {
@@ -541,9 +541,36 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
-            uint16_t* dst = crow + n0 + wv * 128 + f * 32 + h * 16;
-            *reinterpret_cast<uint4*>(dst) = pack8(v);
-            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+            const int col = n0 + wv * 128 + f * 32 + h * 16;
+            if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
+              const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
+              float rf[16];
+              unpack8(*reinterpret_cast<const uint4*>(rr), rf);
+              unpack8(*reinterpret_cast<const uint4*>(rr + 8), rf + 8);
+#pragma unroll
+              for (int i = 0; i < 16; ++i) v[i] = v[i] + rf[i];
+            }
+            if (EPI == 2) {  // accumulate into the fp32 output
+              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float4 o = dst[q];
+                o.x += v[4 * q];
+                o.y += v[4 * q + 1];
+                o.z += v[4 * q + 2];
+                o.w += v[4 * q + 3];
+                dst[q] = o;
+              }
+            } else if (EPI == 3) {  // fp32 partial sums, stored
+              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            } else {
+              uint16_t* dst = crow + col;
+              *reinterpret_cast<uint4*>(dst) = pack8(v);
+              *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+            }
           }
         }
       }
@@ -565,6 +592,23 @@ int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
   const int items_max = (capacity / MT) * (a.n_out / NO);
   int grid = items_max < 256 ? items_max : 256;
   grid = ((grid + 7) / 8) * 8;
+  if constexpr (!GATED && !WEIGHTED) {
+    if (a.epi != 0 && !a.Wp) return GLM52_EUNSUPPORTED;
+    if (a.epi == 1) {
+      moe_gemm_w512_kernel<MT, false, false, true, 1><<<grid, 256, 0, st>>>(a);
+      GLM52_RETURN_LAUNCH();
+    }
+    if (a.epi == 2) {
+      moe_gemm_w512_kernel<MT, false, false, true, 2><<<grid, 256, 0, st>>>(a);
+      GLM52_RETURN_LAUNCH();
+    }
+    if (a.epi == 3) {
+      moe_gemm_w512_kernel<MT, false, false, true, 3><<<grid, 256, 0, st>>>(a);
+      GLM52_RETURN_LAUNCH();
+    }
+  } else {
+    if (a.epi != 0) return GLM52_EUNSUPPORTED;
+  }
   if (a.Wp)
     moe_gemm_w512_kernel<MT, GATED, WEIGHTED, true><<<grid, 256, 0, st>>>(a);
   else
@@ -585,8 +629,9 @@ int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
 // d % 64 of load instruction (d / 64) % 32 of stage (d / 2048) % nk of tile d / (2048 nk).
 template <bool GATED>
 __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restrict__ w,
-                                                        int64_t swe, int64_t swn, int gu_off,
-                                                        int num_n, int nk, int64_t chunks,
+                                                        int64_t swe, int64_t swn, int64_t swk,
+                                                        int gu_off, int num_n, int nk,
+                                                        int64_t chunks,
                                                         uint16_t* __restrict__ out) {
   constexpr int NO = GATED ? 256 : 512;
   for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < chunks;
@@ -599,8 +644,21 @@ __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restri
     const int pid_n = (int)(tile % num_n);
     const int64_t e = tile / num_n;
     const int row = pid_n * NO + w512_row(GATED, gu_off, slot / 8, slot % 8, l);
-    const uint16_t* src = w + e * swe + (int64_t)row * swn + kt * 32 + w512_chunk(l) * 8;
-    *reinterpret_cast<uint4*>(out + d * 8) = *reinterpret_cast<const uint4*>(src);
+    const int64_t k0 = (int64_t)kt * 32 + w512_chunk(l) * 8;
+    const uint16_t* src = w + e * swe + (int64_t)row * swn + k0 * swk;
+    if (swk == 1) {
+      *reinterpret_cast<uint4*>(out + d * 8) = *reinterpret_cast<const uint4*>(src);
+    } else {  // k strided (a [K, N] operand packed as its transpose): gather 8 values
+      uint16_t v[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) v[q] = src[q * swk];
+      uint4 o;
+      o.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+      o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+      o.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+      o.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+      *reinterpret_cast<uint4*>(out + d * 8) = o;
+    }
   }
 }
 
@@ -613,7 +671,8 @@ int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, h
 }
 
 int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_out, int k,
-                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st) {
+                     int gate_up_offset, bool gated, uint16_t* out, hipStream_t st,
+                     int64_t swk) {
   const int NO = gated ? 256 : 512;
   if (E <= 0 || n_out <= 0 || (n_out % NO) || k <= 0 || (k % 64)) return GLM52_EUNSUPPORTED;
   const int num_n = n_out / NO, nk = k / 32;
@@ -623,9 +682,9 @@ int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_o
   const int64_t blocks = (chunks + 255) / 256;
   const int grid = (int)(blocks < 65536 ? blocks : 65536);
   if (gated)
-    pack_w512_kernel<true><<<grid, 256, 0, st>>>(w, swe, swn, gate_up_offset, num_n, nk, chunks, out);
+    pack_w512_kernel<true><<<grid, 256, 0, st>>>(w, swe, swn, swk, gate_up_offset, num_n, nk, chunks, out);
   else
-    pack_w512_kernel<false><<<grid, 256, 0, st>>>(w, swe, swn, 0, num_n, nk, chunks, out);
+    pack_w512_kernel<false><<<grid, 256, 0, st>>>(w, swe, swn, swk, 0, num_n, nk, chunks, out);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? bytes : -(int64_t)err;
 }

@@ -80,3 +80,18 @@ def w13_launch(T: int, n_e: float, shared: bool, route: bool, H: int = C.H, I: i
         cap = -(-(R + E * 15) // 16) * 16
         nbytes += T * E * 4 + E * 4 + R * 8 + 4 * (cap + cap // 16 + 1)
     return KernelCost("w13", 2.0 * rows * H * 2 * I, nbytes)
+
+
+OPROJ_K_DECODE = 32768   # absorbed MLA: 64 heads x 512 (`glm52/config.py:58-59`)
+OPROJ_K_PREFILL = 16384  # 64 heads x 256 (`glm52/config.py:55-56`)
+
+
+def oproj_k(T: int) -> int:
+    """K of o_proj in the reference's regimes: decode batches use the absorbed-MLA width,
+    prefill (T >= 2048) the non-absorbed one (`glm52/config.py:83-88`)."""
+    return OPROJ_K_PREFILL if T >= 2048 else OPROJ_K_DECODE
+
+
+def oproj_cost(T: int, K: int, N: int = C.H) -> KernelCost:
+    """o_proj + ResAdd1, fused: read A [T, K], B [K, N] and r, write h1 [T, N]."""
+    return KernelCost("oproj", 2.0 * T * K * N, K * N * 2 + T * K * 2 + 2 * T * N * 2)

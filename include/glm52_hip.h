@@ -182,6 +182,33 @@ int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row_div, const
                           const int32_t* num_tokens_post_padded, int capacity, int block_m,
                           int num_valid_tokens, int n_out, int k, int gated, hipStream_t stream);
 
+/* o_proj + ResAdd1, the dense GEMM upstream of the block (`glm52/kernels/oproj_resadd.py`).
+ * A [M, K] bf16 (K contiguous), B [K, N] bf16 (strides in elements), r [M, N] bf16.
+ *   glm52_oproj_gemm: c = A @ B with the epilogue of oproj_gemm_kernel: r non-null adds
+ *     the residual (FUSE_RESADD); c_f32 != 0 accumulates into an fp32 c, c += result
+ *     (ATOMIC_OUT, without atomics: one writer per element); else c = bf16(result).
+ *     Replaces oproj_resadd.gemm_launch (glm52/kernels/oproj_resadd.py:144-178).  M <= 16
+ *     with B N-contiguous streams B (split K, fixed-order reduction); otherwise b_packed
+ *     from glm52_oproj_pack is required (N % 512 == 0, K % 64 == 0).  The workspace holds
+ *     glm52_oproj_workspace_bytes(M, N, K) bytes.
+ *   glm52_oproj_pack / glm52_oproj_packed_bytes: B packed once as the 512-row tile
+ *     mapping's W = B^T, cut into `splits` K slices (no counterpart in the reference);
+ *     glm52_oproj_splits(M, N, K) is the count glm52_oproj_gemm wants for that shape
+ *     (more slices when M gives too few 512-row tiles to fill the GPU).
+ *   glm52_cast_add: o = bf16(c (+ r)), c bf16 or fp32 -- oproj_resadd.epilogue_launch
+ *     (glm52/kernels/oproj_resadd.py:181-196). */
+int64_t glm52_oproj_workspace_bytes(int M, int N, int K);
+int glm52_oproj_splits(int M, int N, int K);
+int64_t glm52_oproj_packed_bytes(int K, int N);
+int glm52_oproj_pack(const void* b, int64_t stride_bk, int64_t stride_bn, int K, int N,
+                     int splits, void* packed, hipStream_t stream);
+int glm52_oproj_gemm(const void* a, int64_t stride_am, const void* b, int64_t stride_bk,
+                     int64_t stride_bn, const void* b_packed, int splits, const void* r,
+                     int64_t stride_rm, void* c, int64_t stride_cm, int c_f32, int M, int N,
+                     int K, void* workspace, int64_t workspace_bytes, hipStream_t stream);
+int glm52_cast_add(const void* c, int c_f32, int64_t stride_c, const void* r, int64_t stride_r,
+                   void* o, int64_t stride_o, int M, int N, hipStream_t stream);
+
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */
 int glm52_silu_and_mul(const void* x, int64_t stride_x, void* y, int64_t stride_y, int M, int I,

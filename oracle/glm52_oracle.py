@@ -29,6 +29,8 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   moe_mlp / shared_expert    golden tiny-shape outputs; fp64 textbook GEMM
   block_reference            composition of the above (bench_layer.py:365-374)
   moe_sum / merge_resadd     closed forms (weighted sums) on small shapes
+  oproj_gemm / oproj_cast    one-hot A (exact rows of B, with and without the residual);
+                             fp64 textbook GEMM on small shapes
 """
 
 from __future__ import annotations
@@ -272,6 +274,27 @@ def merge_resadd(y3, wt, res, round_mid: bool = True) -> torch.Tensor:
     if round_mid:
         acc = acc.to(y3.dtype).float()
     return (acc + res.float()).to(y3.dtype)
+
+
+# --------------------------------------------------------------------------------------
+# o_proj + ResAdd1 (upstream of the block)
+# --------------------------------------------------------------------------------------
+def oproj_gemm(a, b, r=None, out_dtype=BF16) -> torch.Tensor:
+    """`oproj_gemm_kernel` (`glm52/kernels/oproj_resadd.py:32-116`): A [M, K] @ B [K, N]
+    accumulated in fp32 (here: fp64, rounded once to fp32), + fp32 r when the residual is
+    fused, one rounding to the output dtype."""
+    acc = (a.double() @ b.double()).float()
+    if r is not None:
+        acc = acc + r.float()
+    return acc.to(out_dtype)
+
+
+def oproj_cast(c, r=None) -> torch.Tensor:
+    """`epilogue_kernel` (`glm52/kernels/oproj_resadd.py:119-136`): bf16(fp32 c (+ fp32 r))."""
+    v = c.float()
+    if r is not None:
+        v = v + r.float()
+    return v.to(BF16)
 
 
 def rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:

@@ -19,6 +19,8 @@ import torch
 from fusion_amd.problem import front_end, zipf_bias
 from oracle import glm52_oracle as O
 
+BF16 = torch.bfloat16
+
 GOLD = Path(__file__).resolve().parent / "golden"
 
 
@@ -346,3 +348,43 @@ def test_merges_closed_form():
     # expert_merge is the round_mid merge without the residual
     assert torch.equal(O.expert_merge(y3, wt),
                        O.merge_resadd(y3, wt, torch.zeros_like(res), round_mid=True))
+
+
+# ------------------------------------------------------------------ o_proj + ResAdd1
+def test_oproj_one_hot_rows_are_exact():
+    """A row with a single 1 at k selects row k of B exactly; with the residual the one
+    fp32 add rounds once to bf16 (closed form)."""
+    g = torch.Generator().manual_seed(3)
+    K, N = 64, 48
+    b = (torch.randn(K, N, generator=g) * 0.3).to(BF16)
+    r = torch.randn(5, N, generator=g).to(BF16)
+    ks = [0, 7, 31, 32, 63]
+    a = torch.zeros(5, K, dtype=BF16)
+    for i, k in enumerate(ks):
+        a[i, k] = 1.0
+    assert torch.equal(O.oproj_gemm(a, b), b[ks])
+    want = (b[ks].float() + r.float()).to(BF16)
+    assert torch.equal(O.oproj_gemm(a, b, r), want)
+    # a scaled one-hot: exact powers of two keep the rows exact
+    assert torch.equal(O.oproj_gemm(a * 4, b), (b[ks].float() * 4).to(BF16))
+
+
+def test_oproj_vs_fp64_textbook_and_cast():
+    g = torch.Generator().manual_seed(4)
+    M, K, N = 6, 96, 40
+    a = (torch.randn(M, K, generator=g) * 0.05).to(BF16)
+    b = (torch.randn(K, N, generator=g) * 0.02).to(BF16)
+    r = (torch.randn(M, N, generator=g) * 0.5).to(BF16)
+    an, bn = a.double().numpy(), b.double().numpy()
+    ref = np.zeros((M, N))
+    for m in range(M):
+        for n in range(N):
+            ref[m, n] = sum(an[m, k] * bn[k, n] for k in range(K))
+    got = O.oproj_gemm(a, b, out_dtype=torch.float32).double().numpy()
+    assert np.abs(got - ref).max() <= 1e-7 * np.abs(ref).max()
+    # fused = cast(unrounded product + r); unfused = cast(bf16 product + r)
+    fused = O.oproj_gemm(a, b, r)
+    assert torch.equal(fused, O.oproj_cast(O.oproj_gemm(a, b, out_dtype=torch.float32), r))
+    unfused = O.oproj_cast(O.oproj_gemm(a, b), r)
+    d = (unfused.float() - fused.float()).abs()
+    assert (d <= fused.float().abs() * 2 ** -7 + 1e-6).all()  # within one extra rounding
