@@ -1,0 +1,96 @@
+"""Half-fused pre-norm (fusion #11b'): drop-in for `glm52/kernels/lazy_prenorm.py`.
+
+The RMSNorm of the block's input h is not materialised for a consumer GEMM: its weight w
+is folded into the consumer's weight once (`fold_weight_rowmajor` / `fold_weight_nk`, the
+reference's load-time transforms, `lazy_prenorm.py:75-85`), and the per-row scale rstd is
+applied to the consumer's accumulator:
+
+    ((h * rstd) * w) @ B  ==  (h @ (w[:, None] * B)) * rstd
+
+Launchers, with the reference's names and arguments:
+
+    launch_rstd(x, rstd, cfg, eps)                         (`lazy_prenorm.py:371-390`)
+    launch_router(a, b, c, cfg, fuse_norm, eps, sq_mode, rstd)        (`:457-...`)
+        c [M, N] fp32 = (a @ b) * rstd   (rstd given, or computed here when fuse_norm)
+    launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                      num_valid_tokens, top_k, cfg, fuse_norm, eps, sq_mode, rstd)
+        c [T * top_k, N] bf16 = bf16((a[f / top_k] @ b[e]^T) * rstd[f / top_k])
+
+`fuse_norm=True` (the fully fused #11, the sum of squares inside the GEMM's k-loop) is
+accepted and computed as the half-fused form: the rstd pass first, then the consumer
+with the rstd epilogue -- the same values.  `sq_mode` selects among Triton reduction
+strategies and is ignored.  rstd's statistic is this build's RMSNorm rule (exact squares
+summed in fp64, one rounding), so it equals the rstd inside `fused_add_rmsnorm`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+from . import moe_gateup as _mg
+from . import norm_router as _nr
+
+
+def fold_weight_rowmajor(b: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """B is [K, N] (contraction dim first): scale ROW k by w[k] (one rounding)."""
+    return (b.float() * w.float()[:, None]).to(b.dtype)
+
+
+def fold_weight_nk(bt: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """B^T is [..., N, K] (nn.Linear / sglang w13 layout): scale COLUMN k by w[k]."""
+    return (bt.float() * w.float()).to(bt.dtype)
+
+
+def smem_bytes(cfg: dict) -> int:
+    """LDS of the consumers that run: the router's token tile (74752 B) and the grouped
+    GEMM's 512-row ring (163840 B); the rstd pass uses none."""
+    return 163840
+
+
+def launch_rstd(x, rstd, cfg, eps: float = 1e-5, rstd_flat=None, repeat: int = 1):
+    """rstd[t] = 1 / sqrt(mean(x[t]^2) + eps) (fp32); `rstd_flat`, if given, receives each
+    value `repeat` times (the per-slot scale of a grouped GEMM with top_k = repeat)."""
+    _lib.require_gpu(x, rstd, rstd_flat)
+    if x.dtype != torch.bfloat16 or x.stride(-1) != 1:
+        raise ValueError("x must be bf16 with its last dim contiguous")
+    for t in (rstd, rstd_flat):
+        if t is not None and (t.dtype != torch.float32 or not t.is_contiguous()):
+            raise ValueError("rstd buffers are contiguous fp32")
+    T, N = x.shape
+    _lib.call("glm52_rstd", _lib.ptr(x), x.stride(0), T, N, float(eps), _lib.ptr(rstd),
+              _lib.ptr(rstd_flat), int(repeat), _lib.stream())
+
+
+def launch_router(a, b, c, cfg, fuse_norm: bool, eps: float = 1e-5, sq_mode: int = 0,
+                  rstd=None):
+    """`a`: [M,K] bf16.  `b`: [K,N] bf16.  `c`: [M,N] fp32."""
+    M = a.shape[0]
+    if fuse_norm and rstd is None:
+        rstd = torch.empty(M, dtype=torch.float32, device=a.device)
+        launch_rstd(a, rstd, cfg, eps)
+    _nr.router_gemm(a, b, c, cfg)
+    if rstd is not None:
+        _lib.require_gpu(rstd)
+        if c.dtype != torch.float32 or c.stride(1) != 1:
+            raise ValueError("c must be fp32 with its last dim contiguous")
+        _lib.call("glm52_scale_rows", _lib.ptr(c), c.stride(0), M, c.shape[1], _lib.ptr(rstd),
+                  _lib.stream())
+
+
+def launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                      num_valid_tokens, top_k, cfg, fuse_norm: bool, eps: float = 1e-5,
+                      sq_mode: int = 0, rstd=None):
+    """`a`: [T,K] bf16.  `b`: [E,N,K] bf16.  `c`: [T*top_k, N] bf16 (gate and up, unfused)."""
+    T = a.shape[0]
+    N = c.shape[1]
+    scale = None
+    if fuse_norm or rstd is not None:
+        # the per-slot scale rstd[f / top_k]; from the given rstd or computed here
+        scale = torch.empty(T * top_k, dtype=torch.float32, device=a.device)
+        if rstd is None:
+            launch_rstd(a, None, cfg, eps, rstd_flat=scale, repeat=top_k)
+        else:
+            scale.view(T, top_k).copy_(rstd.view(T, 1).expand(T, top_k))
+    _mg.moe_gemm(a, top_k, b, c, scale, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                 num_valid_tokens, N, 0, False, cfg)

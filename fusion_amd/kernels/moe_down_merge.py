@@ -37,6 +37,12 @@ def launch_down(a, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
              num_tokens_post_padded, num_valid_tokens, w2.shape[1], 0, False, cfg)
 
 
+def smem_bytes_tokmaj(cfg: dict) -> int:
+    """LDS of the token-major down GEMV (`glm52/kernels/moe_down_merge.py:421-424`), which
+    this build does not implement (see `launch_down_token_major`)."""
+    raise NotImplementedError("token-major down GEMV is not part of this build yet")
+
+
 def launch_down_token_major(a, w2, out, topk_weights, topk_ids, residual, top_k, cfg,
                             add_residual: bool):
     raise NotImplementedError("token-major down GEMV is not part of this build yet")

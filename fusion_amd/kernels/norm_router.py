@@ -122,6 +122,17 @@ def fused_norm_router(x, w, x2, wgt, logits, cfg):
     router_gemm(x2, wgt, logits, cfg)
 
 
+def fused_norm_router_no_x2(x, w, x2, wgt, logits, cfg):
+    """The reference's attribution-only variant (`glm52/kernels/norm_router.py:376-383`):
+    the router logits of norm(x) without storing x2.  The normalised rows go to a scratch
+    buffer (`cfg["x2_scratch"]`, else a temporary); `x2` is left untouched."""
+    scratch = cfg.get("x2_scratch")
+    if scratch is None:
+        scratch = torch.empty_like(x)
+    _an.norm_only(x, w, scratch, cfg)
+    router_gemm(scratch, wgt, logits, cfg)
+
+
 def fused_add_norm_router(x, res, w, h1, x2, wgt, logits, cfg):
     _an.fused_add_rmsnorm(x, res, w, h1, x2, cfg)
     router_gemm(x2, wgt, logits, cfg)

@@ -209,6 +209,18 @@ int glm52_oproj_gemm(const void* a, int64_t stride_am, const void* b, int64_t st
 int glm52_cast_add(const void* c, int c_f32, int64_t stride_c, const void* r, int64_t stride_r,
                    void* o, int64_t stride_o, int M, int N, hipStream_t stream);
 
+/* Half-fused pre-norm (`glm52/kernels/lazy_prenorm.py`, fusion #11b').
+ *   glm52_rstd: rstd[t] = fp32(1 / sqrt(sum_k x[t, k]^2 / N + eps)) for x [T, N] bf16, the
+ *     squares summed in fp64 (the statistic of glm52_add_rmsnorm); rstd_flat, if
+ *     non-null, receives each value `repeat` times.  Replaces rstd_kernel / launch_rstd
+ *     (glm52/kernels/lazy_prenorm.py:346-390).
+ *   glm52_scale_rows: c[t, :] *= rstd[t] (fp32): the router GEMM's USE_RSTD epilogue
+ *     (glm52/kernels/lazy_prenorm.py:323-325), applied after the logits are rounded. */
+int glm52_rstd(const void* x, int64_t stride_x, int T, int N, float eps, float* rstd,
+               float* rstd_flat, int repeat, hipStream_t stream);
+int glm52_scale_rows(float* c, int64_t stride_c, int T, int N, const float* rstd,
+                     hipStream_t stream);
+
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */
 int glm52_silu_and_mul(const void* x, int64_t stride_x, void* y, int64_t stride_y, int M, int I,

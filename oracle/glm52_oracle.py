@@ -31,6 +31,12 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   moe_sum / merge_resadd     closed forms (weighted sums) on small shapes
   oproj_gemm / oproj_cast    one-hot A (exact rows of B, with and without the residual);
                              fp64 textbook GEMM on small shapes
+  rstd_exact                 exact rational sum of squares; constant rows (closed form);
+                             exact halving under h -> 2h at eps = 0; rmsnorm_exact's y
+  fold_weight                power-of-two w (exact), w = 1 (identity), axis choice
+  prenorm_router /           one-hot h (closed form w[k] * b[k] * c * rstd); w = 1 reduces
+  prenorm_gateup_rows        to the plain logits / rows times rstd; the folding identity
+                             against norm -> consumer within the reference's 5e-2 bar
 """
 
 from __future__ import annotations
@@ -81,10 +87,19 @@ def add_rmsnorm_exact(x, residual, w, eps: float = EPS):
     return rmsnorm_exact(h, w, eps), h
 
 
+def rstd_exact(h, eps: float = EPS) -> np.ndarray:
+    """The RMSNorm statistic alone, [T] fp32: fp32(1 / sqrt(sum_k h[t, k]^2 / N + eps)), the
+    exact squares summed in fp64 and rounded once.  The reference's rstd-only kernel
+    (`glm52/kernels/lazy_prenorm.py:347-368`) evaluates the same formula in fp32; the two
+    differ by at most an fp32 ulp or so."""
+    hf = h.float().numpy().astype(np.float64)
+    ss = (hf ** 2).sum(-1)
+    return (1.0 / np.sqrt(ss / hf.shape[-1] + np.float64(np.float32(eps)))).astype(np.float32)
+
+
 def rmsnorm_exact(h, w, eps: float = EPS):
     hf = h.float().numpy()
-    ss = (hf.astype(np.float64) ** 2).sum(-1, keepdims=True)
-    rstd = (1.0 / np.sqrt(ss / hf.shape[-1] + np.float64(np.float32(eps)))).astype(np.float32)
+    rstd = rstd_exact(h, eps)[..., None]
     y = _bf16_round((hf * rstd).astype(np.float32)) * w.float().numpy()
     return torch.from_numpy(y.astype(np.float32)).to(torch.bfloat16)
 
@@ -295,6 +310,39 @@ def oproj_cast(c, r=None) -> torch.Tensor:
     if r is not None:
         v = v + r.float()
     return v.to(BF16)
+
+
+# --------------------------------------------------------------------------------------
+# half-fused pre-norm (lazy_prenorm): the norm weight folded into the consumer weight
+# --------------------------------------------------------------------------------------
+def fold_weight(b, w, k_axis: int) -> torch.Tensor:
+    """`fold_weight_rowmajor` / `fold_weight_nk` (`glm52/kernels/lazy_prenorm.py:75-85`):
+    bf16(fp32 b * fp32 w[k]) along the contraction axis `k_axis` of b."""
+    shape = [1] * b.dim()
+    shape[k_axis] = -1
+    return (b.float() * w.float().reshape(shape)).to(b.dtype)
+
+
+def prenorm_router(h, b_fold, rstd) -> np.ndarray:
+    """`router_gemm_kernel` with USE_RSTD (`lazy_prenorm.py:229-330`): fp32 logits of
+    h @ b_fold under the order-independent rule, then one fp32 multiply by rstd[t]."""
+    lg = router_logits_exact(h, b_fold)
+    return (lg * np.asarray(rstd, dtype=np.float32)[:, None]).astype(np.float32)
+
+
+def prenorm_gateup_rows(h, w_fold, rstd, topk_ids) -> torch.Tensor:
+    """`moe_gateup_prenorm_kernel` with USE_RSTD (`lazy_prenorm.py:89-226`), no activation:
+    slot f = t * top_k + j holds bf16(fp32(h[t] @ w_fold[topk_ids[t, j]]^T) * rstd[t]),
+    the accumulator in fp64 rounded once to fp32.  Returns [T * top_k, N] bf16."""
+    T, k = topk_ids.shape
+    hd = h.double()
+    out = torch.empty(T * k, w_fold.shape[1], dtype=torch.float32)
+    r = torch.from_numpy(np.asarray(rstd, dtype=np.float32))
+    for t in range(T):
+        for j in range(k):
+            acc = (w_fold[int(topk_ids[t, j])].double() @ hd[t]).float()
+            out[t * k + j] = acc * r[t]
+    return out.to(BF16)
 
 
 def rel_err(got: torch.Tensor, ref: torch.Tensor) -> float:

@@ -388,3 +388,97 @@ def test_oproj_vs_fp64_textbook_and_cast():
     unfused = O.oproj_cast(O.oproj_gemm(a, b), r)
     d = (unfused.float() - fused.float()).abs()
     assert (d <= fused.float().abs() * 2 ** -7 + 1e-6).all()  # within one extra rounding
+
+
+# ------------------------------------------------------------------ half-fused pre-norm
+def test_rstd_exact_rational_sum_and_closed_forms():
+    g = torch.Generator().manual_seed(21)
+    h = torch.randn(4, 192, generator=g).to(BF16)
+    r = O.rstd_exact(h)
+    for t in range(4):
+        ss = sum(Fraction(float(v)) ** 2 for v in h[t].float().tolist())
+        want = np.float32(1.0 / np.sqrt(float(ss / 192) + float(np.float32(1e-5))))
+        assert r[t] == want
+    # constant rows: rstd = 1 / sqrt(c^2 + eps)
+    for c in (0.5, -3.0, 7.25):
+        x = torch.full((1, 64), c, dtype=BF16)
+        assert O.rstd_exact(x)[0] == np.float32(1.0 / np.sqrt(c * c + float(np.float32(1e-5))))
+    # eps = 0: doubling the row halves rstd exactly
+    assert np.array_equal(O.rstd_exact(h * 2, eps=0.0), O.rstd_exact(h, eps=0.0) / 2)
+    # the statistic inside rmsnorm_exact (w = 1: y = bf16(h * rstd))
+    y = O.rmsnorm_exact(h, torch.ones(192, dtype=BF16))
+    assert torch.equal(y, (h.float() * torch.from_numpy(r)[:, None]).to(BF16))
+
+
+def test_fold_weight_axes_and_exact_cases():
+    g = torch.Generator().manual_seed(22)
+    b = torch.randn(64, 24, generator=g).to(BF16)
+    w = torch.full((64,), 2.0, dtype=BF16)
+    assert torch.equal(O.fold_weight(b, w, 0), (b.float() * 2).to(BF16))
+    assert torch.equal(O.fold_weight(b, torch.ones(64, dtype=BF16), 0), b)
+    w = (1 + 0.1 * torch.randn(64, generator=g)).to(BF16)
+    bt = b.t().contiguous()
+    assert torch.equal(O.fold_weight(b, w, 0).t(), O.fold_weight(bt, w, 1))
+    assert torch.equal(O.fold_weight(b, w, 0)[5], (b[5].float() * w[5].float()).to(BF16))
+
+
+def test_prenorm_router_one_hot_and_identity():
+    g = torch.Generator().manual_seed(23)
+    K, N = 128, 32
+    b = (torch.randn(K, N, generator=g) * 0.02).to(BF16)
+    w = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    bf = O.fold_weight(b, w, 0)
+    # one-hot rows: the logits are fp32(bf[k] * c) * rstd, rstd = 1 / sqrt(c^2 / K + eps)
+    ks, c = [0, 17, 127], 3.0
+    h = torch.zeros(3, K, dtype=BF16)
+    for i, k in enumerate(ks):
+        h[i, k] = c
+    rstd = O.rstd_exact(h)
+    assert np.all(rstd == np.float32(1.0 / np.sqrt(c * c / K + float(np.float32(1e-5)))))
+    got = O.prenorm_router(h, bf, rstd)
+    want = (bf[ks].float().numpy() * np.float32(c)) * rstd[:, None]
+    assert np.array_equal(got, want.astype(np.float32))
+    # w = 1 folds to the plain weight: the logits times rstd
+    hr = (torch.randn(5, K, generator=g) * 0.5).to(BF16)
+    rr = O.rstd_exact(hr)
+    plain = O.router_logits_exact(hr, b)
+    assert np.array_equal(O.prenorm_router(hr, O.fold_weight(b, torch.ones(K, dtype=BF16), 0), rr),
+                          (plain * rr[:, None]).astype(np.float32))
+    # the folding identity against norm -> router (`bench_f11_lazy_prenorm.py:996-1014`)
+    un = O.router_logits_exact(O.rmsnorm_exact(hr, w), b)
+    assert O.rel_err(torch.from_numpy(O.prenorm_router(hr, bf, rr)), torch.from_numpy(un)) < 5e-2
+
+
+def test_prenorm_gateup_rows_one_hot_and_identity():
+    g = torch.Generator().manual_seed(24)
+    T, K, N, E, k = 3, 64, 32, 4, 2
+    w13 = (torch.randn(E, N, K, generator=g) * 0.02).to(BF16)
+    wn = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    wf = O.fold_weight(w13, wn, 2)
+    ids = torch.tensor([[0, 3], [2, 1], [3, 0]])
+    h = (torch.randn(T, K, generator=g) * 0.5).to(BF16)
+    r = O.rstd_exact(h)
+    got = O.prenorm_gateup_rows(h, wf, r, ids)
+    # textbook per slot: an exact rational dot product, rounded to fp32, times rstd
+    for t in range(T):
+        for j in range(k):
+            e = int(ids[t, j])
+            for n_ in (0, 13, N - 1):
+                dot = sum(Fraction(float(wf[e, n_, q])) * Fraction(float(h[t, q]))
+                          for q in range(K))
+                want = torch.tensor(np.float32(np.float32(float(dot)) * r[t])).to(BF16)
+                assert torch.equal(got[t * k + j, n_], want)
+    # one-hot h: slot rows are bf16(fp32(wf[e, :, kk] * c) * rstd)
+    c, kk = 2.0, 9
+    h1 = torch.zeros(1, K, dtype=BF16)
+    h1[0, kk] = c
+    r1 = O.rstd_exact(h1)
+    got1 = O.prenorm_gateup_rows(h1, wf, r1, ids[:1])
+    for j in range(k):
+        e = int(ids[0, j])
+        want = ((wf[e, :, kk].float() * c) * float(r1[0])).to(BF16)
+        assert torch.equal(got1[j], want)
+    # the folding identity against norm -> gate/up GEMM on the raw weight
+    x2 = O.rmsnorm_exact(h, wn)
+    un = O.prenorm_gateup_rows(x2, w13, np.ones(T, dtype=np.float32), ids)
+    assert O.rel_err(got, un) < 5e-2
