@@ -48,7 +48,7 @@ def parse():
     ap.add_argument("--calibrate", action="store_true",
                     help="only measure the read-bandwidth ceiling (glm52_stream_read) and exit")
     ap.add_argument("--no-oproj", action="store_true",
-                    help="skip the o_proj + ResAdd1 timing reported beside each T")
+                    help="skip the o_proj + ResAdd1 and pre-norm router timings reported beside each T")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 --pmc child runs behind roofline.traffic")
     ap.add_argument("--pmc-child", action="store_true",
@@ -176,6 +176,7 @@ def main() -> int:
         }
         if not args.no_oproj:
             rec["oproj"] = oproj_bench(T, timed, args.steps, args.warmup, dev)
+            rec["prenorm_router"] = prenorm_bench(T, timed, args.steps, args.warmup, dev)
         per_T[str(T)] = rec
         log(f"T={T}: {rec}")
         if headline is None:
@@ -320,6 +321,61 @@ def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
             "roofline_frac": round(roof / us, 4), "bound": kc.bound(),
             "GBps": round(kc.bytes / (us * 1e-6) / 1e9, 1),
             "TFLOPs": round(kc.flops / (us * 1e-6) / 1e12, 1)}
+
+
+def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
+    """The half-fused pre-norm router beside the unfused one (upstream of the block's own
+    front end, not part of `value`), on the reference's #11b problem
+    (`glm52/prof/prof_f11b.py:27-46`): unfused = RMSNorm into x2, then the router on the
+    raw gate; half-fused = the rstd pass, then the router on the folded gate with the rstd
+    epilogue; fused = `fuse_norm=True` (one launch at T <= 4).  The gate is read as [E, H]
+    rows at T <= 16 and as [H, E] above, as in the block.  The roofline counts bytes only
+    (the bf16 MFMA bound of the router's flops is below them at every T)."""
+    import torch
+
+    from fusion_amd import roofline as RL
+    from fusion_amd.kernels import add_rmsnorm as KN
+    from fusion_amd.kernels import lazy_prenorm as KL
+
+    H, E = 6144, 256
+    g = torch.Generator(device=dev).manual_seed(0)
+    h1 = (torch.randn(T, H, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    w = (torch.randn(H, device=dev, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    gate = (torch.randn(E, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    gate_f = KL.fold_weight_nk(gate, w)
+    if T <= 16:
+        b_raw, b_fold = gate.t(), gate_f.t()
+    else:
+        b_raw, b_fold = gate.t().contiguous(), gate_f.t().contiguous()
+    x2 = torch.empty_like(h1)
+    rstd = torch.empty(T, device=dev, dtype=torch.float32)
+    lg = torch.empty(T, E, device=dev, dtype=torch.float32)
+
+    def unfused():
+        KN.norm_only(h1, w, x2, {})
+        KL.launch_router(x2, b_raw, lg, {}, False)
+
+    def half():
+        KL.launch_rstd(h1, rstd, {})
+        KL.launch_router(h1, b_fold, lg, {}, False, 1e-5, 0, rstd)
+
+    def fused():  # one launch at T <= 4 (gate rows); the half-fused pair above that
+        KL.launch_router(h1, b_fold, lg, {}, True)
+
+    u_ms, _ = timed(unfused, steps, warmup)
+    h_ms, _ = timed(half, steps, warmup)
+    f_ms, _ = timed(fused, steps, warmup)
+    u_us, h_us = statistics.median(u_ms) * 1e3, statistics.median(h_ms) * 1e3
+    f_us = statistics.median(f_ms) * 1e3
+    act = T * H * 2
+    # half-fused: the rstd pass reads act; the router reads act and the gate, writes logits
+    kc = RL.KernelCost("prenorm_router", 2.0 * T * H * E, 2 * act + H * E * 2 + T * E * 4)
+    roof = kc.seconds() * 1e6
+    del h1, x2, gate, gate_f, b_raw, b_fold, lg
+    return {"unfused_us": round(u_us, 2), "half_fused_us": round(h_us, 2),
+            "fused_us": round(f_us, 2), "gain": round(u_us / min(h_us, f_us), 3),
+            "roofline_us": round(roof, 2), "roofline_frac": round(roof / min(h_us, f_us), 4),
+            "bound": kc.bound()}
 
 
 def calibrate(dev) -> list:

@@ -117,9 +117,32 @@ __global__ __launch_bounds__(256) void oproj_splitk_kernel(
   }
 }
 
-// One wave per (row t, 8-column chunk): the S partials (split sp of row t at
-// ws + sp s_split + t s_tok) added in a fixed order, then the epilogue (0: bf16; 1: + r,
-// bf16; 2: c32 += sum (+ r)).
+// The epilogue of a reduced 8-column chunk of row t (0: bf16; 1: + r, bf16; 2: c32 += sum
+// (+ r)).
+__device__ inline void reduce_store(float (&v)[kCols], int t, int ch,
+                                    const uint16_t* __restrict__ r, int64_t srm,
+                                    uint16_t* __restrict__ c, float* __restrict__ c32,
+                                    int64_t scm, int epi) {
+  if (r && epi != 0) {
+    float rf[kCols];
+    unpack8(*reinterpret_cast<const uint4*>(r + (int64_t)t * srm + ch * kCols), rf);
+#pragma unroll
+    for (int q = 0; q < kCols; ++q) v[q] = v[q] + rf[q];
+  }
+  if (epi == 2) {
+    float4* dst = reinterpret_cast<float4*>(c32 + (int64_t)t * scm + ch * kCols);
+    float4 o0 = dst[0], o1 = dst[1];
+    o0.x += v[0]; o0.y += v[1]; o0.z += v[2]; o0.w += v[3];
+    o1.x += v[4]; o1.y += v[5]; o1.z += v[6]; o1.w += v[7];
+    dst[0] = o0;
+    dst[1] = o1;
+  } else {
+    *reinterpret_cast<uint4*>(c + (int64_t)t * scm + ch * kCols) = pack8(v);
+  }
+}
+
+// Many splits (decode): one wave per (row t, 8-column chunk); lane l adds the partials
+// l, l + 64, ... (split sp of row t at ws + sp s_split + t s_tok), then a fixed butterfly.
 __global__ __launch_bounds__(256) void oproj_reduce_kernel(
     const float* __restrict__ ws, int64_t s_split, int64_t s_tok, int S, int M, int N,
     const uint16_t* __restrict__ r, int64_t srm, uint16_t* __restrict__ c,
@@ -141,22 +164,60 @@ __global__ __launch_bounds__(256) void oproj_reduce_kernel(
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v[q] += __shfl_xor(v[q], off, kWave);
   if (lane != 0) return;
-  if (r && epi != 0) {
-    float rf[kCols];
-    unpack8(*reinterpret_cast<const uint4*>(r + (int64_t)t * srm + ch * kCols), rf);
+  reduce_store(v, t, ch, r, srm, c, c32, scm, epi);
+}
+
+// Few splits (the prefill K slices): one thread per (row t, 8-column chunk), the S
+// partials added in split order, 8 of them loaded before the first add.
+constexpr int kSeqSplits = 32;  // at most this many splits take this kernel
+
+__global__ __launch_bounds__(256) void oproj_reduce_seq_kernel(
+    const float* __restrict__ ws, int64_t s_split, int64_t s_tok, int S, int M, int N,
+    const uint16_t* __restrict__ r, int64_t srm, uint16_t* __restrict__ c,
+    float* __restrict__ c32, int64_t scm, int epi) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int nchunk = N / kCols;
+  if (q >= (int64_t)M * nchunk) return;
+  const int t = (int)(q / nchunk), ch = (int)(q % nchunk);
+  const float* base = ws + t * s_tok + ch * kCols;
+  float v[kCols] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int sp0 = 0; sp0 < S; sp0 += 8) {
+    float4 p[8][2];
 #pragma unroll
-    for (int q = 0; q < kCols; ++q) v[q] = v[q] + rf[q];
+    for (int i = 0; i < 8; ++i) {
+      if (sp0 + i < S) {
+        const float4* src = reinterpret_cast<const float4*>(base + (int64_t)(sp0 + i) * s_split);
+        p[i][0] = src[0];
+        p[i][1] = src[1];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      if (sp0 + i < S) {
+        v[0] += p[i][0].x; v[1] += p[i][0].y; v[2] += p[i][0].z; v[3] += p[i][0].w;
+        v[4] += p[i][1].x; v[5] += p[i][1].y; v[6] += p[i][1].z; v[7] += p[i][1].w;
+      }
+    }
   }
-  if (epi == 2) {
-    float4* dst = reinterpret_cast<float4*>(c32 + (int64_t)t * scm + ch * kCols);
-    float4 o0 = dst[0], o1 = dst[1];
-    o0.x += v[0]; o0.y += v[1]; o0.z += v[2]; o0.w += v[3];
-    o1.x += v[4]; o1.y += v[5]; o1.z += v[6]; o1.w += v[7];
-    dst[0] = o0;
-    dst[1] = o1;
-  } else {
-    *reinterpret_cast<uint4*>(c + (int64_t)t * scm + ch * kCols) = pack8(v);
-  }
+  reduce_store(v, t, ch, r, srm, c, c32, scm, epi);
+}
+
+// The fixed-order sum of S split partials with the epilogue; the mapping is a function of
+// S alone, so a shape always sums in the same order.
+hipError_t launch_reduce(const float* ws, int64_t s_split, int64_t s_tok, int S, int M, int N,
+                         const void* r, int64_t srm, void* c, int64_t scm, int epi,
+                         hipStream_t stream) {
+  const int64_t items = (int64_t)M * (N / kCols);
+  const auto* rr = static_cast<const uint16_t*>(r);
+  if (S <= kSeqSplits)
+    oproj_reduce_seq_kernel<<<(int)((items + 255) / 256), 256, 0, stream>>>(
+        ws, s_split, s_tok, S, M, N, rr, srm, static_cast<uint16_t*>(c), static_cast<float*>(c),
+        scm, epi);
+  else
+    oproj_reduce_kernel<<<(int)((items + 3) / 4), 256, 0, stream>>>(
+        ws, s_split, s_tok, S, M, N, rr, srm, static_cast<uint16_t*>(c), static_cast<float*>(c),
+        scm, epi);
+  return hipGetLastError();
 }
 
 // The row layout of an M-row dense GEMM split S ways along K, on block size BM: "expert"
@@ -320,11 +381,9 @@ extern "C" int glm52_oproj_gemm(const void* a, int64_t stride_am, const void* b,
       oproj_splitk_kernel<16, 1, 8><<<grid, 256, 0, stream>>>(aa, stride_am, bb, stride_bk, M, N, K, sp.KC, ws);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return (int)err;
-    const int64_t waves = (int64_t)M * (N / kCols);
-    oproj_reduce_kernel<<<(int)((waves + 3) / 4), 256, 0, stream>>>(
-        ws, (int64_t)M * N, N, sp.S, M, N, static_cast<const uint16_t*>(r), stride_rm,
-        static_cast<uint16_t*>(c), static_cast<float*>(c), stride_cm, epi);
-    GLM52_RETURN_LAUNCH();
+    const hipError_t rerr = launch_reduce(ws, (int64_t)M * N, N, sp.S, M, N, r, stride_rm, c,
+                                          stride_cm, epi, stream);
+    return rerr == hipSuccess ? GLM52_OK : (int)rerr;
   }
   if (!b_packed || !al16(b_packed)) return GLM52_EUNSUPPORTED;
   const int S = splits;
@@ -366,11 +425,9 @@ extern "C" int glm52_oproj_gemm(const void* a, int64_t stride_am, const void* b,
   g.scm = N;
   const int rc = launch_wide512(g, cap, false, false, stream);
   if (rc != GLM52_OK) return rc;
-  const int64_t waves = (int64_t)M * (N / kCols);
-  oproj_reduce_kernel<<<(int)((waves + 3) / 4), 256, 0, stream>>>(
-      part, N, (int64_t)S * N, S, M, N, static_cast<const uint16_t*>(r), stride_rm,
-      static_cast<uint16_t*>(c), static_cast<float*>(c), stride_cm, epi);
-  GLM52_RETURN_LAUNCH();
+  const hipError_t rerr = launch_reduce(part, N, (int64_t)S * N, S, M, N, r, stride_rm, c,
+                                        stride_cm, epi, stream);
+  return rerr == hipSuccess ? GLM52_OK : (int)rerr;
 }
 
 // o = bf16(c (+ r)): `epilogue_kernel` (c bf16 or fp32).

@@ -65,7 +65,8 @@ GLM52_DEV int gsw(int c) { return ((c >> 2) ^ (c >> 3)) & 1; }
 template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_logits_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swg,
-    float* __restrict__ logits, int64_t sl, double* __restrict__ part, int T, int H, int E) {
+    float* __restrict__ logits, int64_t sl, double* __restrict__ part, int T, int H, int E,
+    const float* __restrict__ rstd) {
   using WT = typename std::conditional<WG_F32, float, uint16_t>::type;
   constexpr int EPV = 16 / sizeof(WT);        // gate entries per 16-byte vector
   constexpr int CPR = EMAX / EPV;              // 16-byte vectors per gate row (32 or 64)
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   for (int q = tid; q < nt * E; q += 256) {
     const int tl = q / E, e = q % E;
     const double s = st[tl * EMAX + e];
-    if (KS == 1) logits[(int64_t)(t0 + tl) * sl + e] = (float)s;
+    if (KS == 1) logits[(int64_t)(t0 + tl) * sl + e] = rstd ? (float)s * rstd[t0 + tl] : (float)s;
     else part[((int64_t)blockIdx.y * T + t0 + tl) * E + e] = s;
   }
 }
@@ -193,7 +194,7 @@ constexpr int HMAX = 8192;
 template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_rows_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swe,
-    float* __restrict__ logits, int64_t sl, int T, int H, int E) {
+    float* __restrict__ logits, int64_t sl, int T, int H, int E, const float* __restrict__ rstd) {
   extern __shared__ __attribute__((aligned(16))) uint16_t ys[];  // [min(RT, T - t0)][H]
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -237,15 +238,16 @@ __global__ __launch_bounds__(256) void router_rows_kernel(
   for (int t = 0; t < RT; ++t) {
     if (t < nt) {  // each reduction is 12 cross-lane moves: only the tokens that exist
       const double s = wave_sum_f64(acc[t]);
-      if (lane == 0) logits[(int64_t)(t0 + t) * sl + e] = (float)s;
+      if (lane == 0) logits[(int64_t)(t0 + t) * sl + e] = rstd ? (float)s * rstd[t0 + t] : (float)s;
     }
   }
 }
 
-// logits[t, e] = fp32(sum_ks part[ks, t, e]), ks in order.
+// logits[t, e] = fp32(sum_ks part[ks, t, e]), ks in order (times rstd[t] if given).
 __global__ __launch_bounds__(256) void router_reduce_kernel(const double* __restrict__ part,
                                                             float* __restrict__ logits,
-                                                            int64_t sl, int T, int E, int KS) {
+                                                            int64_t sl, int T, int E, int KS,
+                                                            const float* __restrict__ rstd) {
   const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (q >= (int64_t)T * E) return;
   const int64_t t = q / E;
@@ -259,7 +261,7 @@ __global__ __launch_bounds__(256) void router_reduce_kernel(const double* __rest
     for (int i = 0; i < 8; ++i)
       if (ks0 + i < KS) s += v[i];
   }
-  logits[t * sl + e] = (float)s;
+  logits[t * sl + e] = rstd ? (float)s * rstd[t] : (float)s;
 }
 
 // One wave per token, four tokens per workgroup.  If `part` is non-null the fp64
@@ -333,7 +335,7 @@ namespace {
 int launch_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
                   int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
                   void* workspace, int64_t workspace_bytes, int T, int H, int E, int* ks_out,
-                  hipStream_t stream) {
+                  hipStream_t stream, const float* rstd = nullptr) {
   if (T < 0 || H <= 0 || E <= 0 || E > EMAX || (E % 16) != 0 || (H % KC) != 0) return GLM52_EINVAL;
   if (!y || !wgt || !logits || stride_l < E || stride_y < H || (stride_y % 8) ||
       (reinterpret_cast<uintptr_t>(y) & 15u))
@@ -349,9 +351,9 @@ int launch_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stri
     const size_t lds = (size_t)(T < RT ? T : RT) * H * sizeof(uint16_t);  // <= 64 KB
     auto* yy = static_cast<const uint16_t*>(y);
     if (wg_is_f32)
-      router_rows_kernel<true><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E);
+      router_rows_kernel<true><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
     else
-      router_rows_kernel<false><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E);
+      router_rows_kernel<false><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
     GLM52_RETURN_LAUNCH();
   }
   if (stride_we != 1 || stride_wk < E || (stride_wk % vec)) return GLM52_EINVAL;
@@ -365,9 +367,25 @@ int launch_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stri
   auto* yy = static_cast<const uint16_t*>(y);
   auto* part = static_cast<double*>(workspace);
   if (wg_is_f32)
-    router_logits_kernel<true><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E);
+    router_logits_kernel<true><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E, rstd);
   else
-    router_logits_kernel<false><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E);
+    router_logits_kernel<false><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_wg, logits, stride_l, part, T, H, E, rstd);
+  GLM52_RETURN_LAUNCH();
+}
+}  // namespace
+
+namespace {
+int logits_entry(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                 int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                 void* workspace, int64_t workspace_bytes, int T, int H, int E,
+                 const float* rstd, hipStream_t stream) {
+  int ks = 1;
+  int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                         workspace, workspace_bytes, T, H, E, &ks, stream, rstd);
+  if (rc != GLM52_OK || T == 0 || ks == 1) return rc;
+  const int64_t n = (int64_t)T * E;
+  router_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+      static_cast<const double*>(workspace), logits, stride_l, T, E, ks, rstd);
   GLM52_RETURN_LAUNCH();
 }
 }  // namespace
@@ -377,14 +395,20 @@ extern "C" int glm52_router_logits(const void* y, int64_t stride_y, const void* 
                                    float* logits, int64_t stride_l, void* workspace,
                                    int64_t workspace_bytes, int T, int H, int E,
                                    hipStream_t stream) {
-  int ks = 1;
-  int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
-                         workspace, workspace_bytes, T, H, E, &ks, stream);
-  if (rc != GLM52_OK || T == 0 || ks == 1) return rc;
-  const int64_t n = (int64_t)T * E;
-  router_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
-      static_cast<const double*>(workspace), logits, stride_l, T, E, ks);
-  GLM52_RETURN_LAUNCH();
+  return logits_entry(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                      workspace, workspace_bytes, T, H, E, nullptr, stream);
+}
+
+// The router GEMM with the half-fused pre-norm epilogue: each logit is rounded to fp32 as
+// in glm52_router_logits, then multiplied by rstd[t] (one fp32 product) before its store.
+extern "C" int glm52_router_logits_rstd(const void* y, int64_t stride_y, const void* wgt,
+                                        int64_t stride_wk, int64_t stride_we, int wg_is_f32,
+                                        const float* rstd, float* logits, int64_t stride_l,
+                                        void* workspace, int64_t workspace_bytes, int T, int H,
+                                        int E, hipStream_t stream) {
+  if (T > 0 && !rstd) return GLM52_EINVAL;
+  return logits_entry(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                      workspace, workspace_bytes, T, H, E, rstd, stream);
 }
 
 extern "C" int glm52_router_topk(const float* logits, int64_t stride_l, const float* bias,

@@ -10,15 +10,17 @@ applied to the consumer's accumulator:
 Launchers, with the reference's names and arguments:
 
     launch_rstd(x, rstd, cfg, eps)                         (`lazy_prenorm.py:371-390`)
-    launch_router(a, b, c, cfg, fuse_norm, eps, sq_mode, rstd)        (`:457-...`)
-        c [M, N] fp32 = (a @ b) * rstd   (rstd given, or computed here when fuse_norm)
+    launch_router(a, b, c, cfg, fuse_norm, eps, sq_mode, rstd)        (`:457-489`)
+        c [M, N] fp32 = (a @ b) * rstd   (rstd given, or computed here when fuse_norm);
+        the logits rounded to fp32 under the router's exact rule, then one fp32 product
     launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
                       num_valid_tokens, top_k, cfg, fuse_norm, eps, sq_mode, rstd)
         c [T * top_k, N] bf16 = bf16((a[f / top_k] @ b[e]^T) * rstd[f / top_k])
 
-`fuse_norm=True` (the fully fused #11, the sum of squares inside the GEMM's k-loop) is
-accepted and computed as the half-fused form: the rstd pass first, then the consumer
-with the rstd epilogue -- the same values.  `sq_mode` selects among Triton reduction
+`fuse_norm=True` (the fully fused #11, the sum of squares inside the GEMM's k-loop) runs
+fully fused for the router at T <= 4 on a gate read as rows (one launch: the statistic and
+the dot in the same pass over h); elsewhere it is computed as the half-fused form, the
+rstd pass first, then the consumer with the rstd epilogue -- the same values.  `sq_mode` selects among Triton reduction
 strategies and is ignored.  rstd's statistic is this build's RMSNorm rule (exact squares
 summed in fp64, one rounding), so it equals the rstd inside `fused_add_rmsnorm`.
 """
@@ -66,16 +68,39 @@ def launch_router(a, b, c, cfg, fuse_norm: bool, eps: float = 1e-5, sq_mode: int
                   rstd=None):
     """`a`: [M,K] bf16.  `b`: [K,N] bf16.  `c`: [M,N] fp32."""
     M = a.shape[0]
+    if (fuse_norm or rstd is not None) and M <= 4 and b.stride(0) == 1:
+        _rows_router(a, b, c, rstd, eps)
+        return
     if fuse_norm and rstd is None:
         rstd = torch.empty(M, dtype=torch.float32, device=a.device)
         launch_rstd(a, rstd, cfg, eps)
-    _nr.router_gemm(a, b, c, cfg)
-    if rstd is not None:
-        _lib.require_gpu(rstd)
-        if c.dtype != torch.float32 or c.stride(1) != 1:
-            raise ValueError("c must be fp32 with its last dim contiguous")
-        _lib.call("glm52_scale_rows", _lib.ptr(c), c.stride(0), M, c.shape[1], _lib.ptr(rstd),
-                  _lib.stream())
+    if rstd is None:
+        _nr.router_gemm(a, b, c, cfg)
+        return
+    _nr._check_router_operands(a, b, c)
+    _lib.require_gpu(rstd)
+    if rstd.dtype != torch.float32 or not rstd.is_contiguous() or rstd.numel() < M:
+        raise ValueError("rstd must be a contiguous fp32 tensor of M values")
+    K, N = a.shape[1], b.shape[1]
+    ws, need = _nr._workspace(M, K, N, a.device, cfg, b)
+    _lib.call("glm52_router_logits_rstd", _lib.ptr(a), a.stride(0), _lib.ptr(b), b.stride(0),
+              b.stride(1), int(b.dtype == torch.float32), _lib.ptr(rstd), _lib.ptr(c),
+              c.stride(0), _lib.ptr(ws), need, M, K, N, _lib.stream())
+
+
+def _rows_router(a, b, c, rstd, eps):
+    """T <= 4 on a gate read as rows (b = the transposed view of a [N, K] gate): one launch,
+    the statistic computed in the same pass when rstd is None."""
+    _nr._check_router_operands(a, b, c)
+    _lib.require_gpu(rstd)
+    if b.dtype != torch.bfloat16:
+        raise ValueError("the decode pre-norm router reads a bf16 gate")
+    if rstd is not None and (rstd.dtype != torch.float32 or not rstd.is_contiguous()):
+        raise ValueError("rstd must be a contiguous fp32 tensor")
+    M, K = a.shape
+    _lib.call("glm52_prenorm_router_rows", _lib.ptr(a), a.stride(0), _lib.ptr(b), b.stride(1),
+              _lib.ptr(rstd), float(eps), _lib.ptr(c), c.stride(0), 0, M, K, b.shape[1],
+              _lib.stream())
 
 
 def launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_padded,

@@ -214,12 +214,22 @@ int glm52_cast_add(const void* c, int c_f32, int64_t stride_c, const void* r, in
  *     squares summed in fp64 (the statistic of glm52_add_rmsnorm); rstd_flat, if
  *     non-null, receives each value `repeat` times.  Replaces rstd_kernel / launch_rstd
  *     (glm52/kernels/lazy_prenorm.py:346-390).
- *   glm52_scale_rows: c[t, :] *= rstd[t] (fp32): the router GEMM's USE_RSTD epilogue
- *     (glm52/kernels/lazy_prenorm.py:323-325), applied after the logits are rounded. */
+ *   glm52_router_logits_rstd: glm52_router_logits with the USE_RSTD epilogue of the
+ *     reference's router GEMM (glm52/kernels/lazy_prenorm.py:229-330, launch_router :457):
+ *     each logit, rounded to fp32, times rstd[t] (one fp32 product) before its store. */
 int glm52_rstd(const void* x, int64_t stride_x, int T, int N, float eps, float* rstd,
                float* rstd_flat, int repeat, hipStream_t stream);
-int glm52_scale_rows(float* c, int64_t stride_c, int T, int N, const float* rstd,
-                     hipStream_t stream);
+/* glm52_prenorm_router_rows: the same router for T <= 4 tokens on a gate read as rows
+ *     ([E, H], the transposed view of the [H, E] operand): one workgroup per gate row; when
+ *     rstd_in is null the statistic is computed in the same pass over h (the reference's
+ *     FUSE_NORM, lazy_prenorm.py:300-322) and written to rstd_out if that is non-null. */
+int glm52_prenorm_router_rows(const void* h, int64_t stride_h, const void* gate, int64_t stride_g,
+                              const float* rstd_in, float eps, float* logits, int64_t stride_l,
+                              float* rstd_out, int T, int H, int E, hipStream_t stream);
+int glm52_router_logits_rstd(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                             int64_t stride_we, int wg_is_f32, const float* rstd, float* logits,
+                             int64_t stride_l, void* workspace, int64_t workspace_bytes, int T,
+                             int H, int E, hipStream_t stream);
 
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */

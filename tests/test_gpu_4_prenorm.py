@@ -67,13 +67,22 @@ def test_rstd_strided_rows_and_empty(gpu):
     assert np.array_equal(rstd.cpu().numpy(), O.rstd_exact(view.cpu(), EPS))
 
 
-@pytest.mark.parametrize("T", [1, 4, 64, 1000])
-def test_prenorm_router_bitwise(gpu, T):
-    say(f"prenorm router T={T}")
+@pytest.mark.parametrize("layout", ["kn", "rows"])
+@pytest.mark.parametrize("T", [1, 3, 4, 7, 64, 1000])
+def test_prenorm_router_bitwise(gpu, T, layout):
+    """`kn`: B [K, N] contiguous, as the reference passes it; `rows`: B the transposed view
+    of the [N, K] gate (the one-launch fully fused mapping at T <= 4)."""
+    say(f"prenorm router T={T} {layout}")
     h, w, g = _h(T, gpu, 80 + T)
-    b_raw = (torch.randn(H, ER, device=gpu, generator=g) * 0.02).to(BF16)
-    b_fold = KL.fold_weight_rowmajor(b_raw, w)
-    assert torch.equal(b_fold.cpu(), O.fold_weight(b_raw.cpu(), w.cpu(), 0))
+    if layout == "kn":
+        b_raw = (torch.randn(H, ER, device=gpu, generator=g) * 0.02).to(BF16)
+        b_fold = KL.fold_weight_rowmajor(b_raw, w)
+        assert torch.equal(b_fold.cpu(), O.fold_weight(b_raw.cpu(), w.cpu(), 0))
+    else:
+        gate = (torch.randn(ER, H, device=gpu, generator=g) * 0.02).to(BF16)
+        gate_f = KL.fold_weight_nk(gate, w)
+        assert torch.equal(gate_f.cpu(), O.fold_weight(gate.cpu(), w.cpu(), 1))
+        b_raw, b_fold = gate.t(), gate_f.t()
     rstd = torch.empty(T, device=gpu)
     KL.launch_rstd(h, rstd, {}, EPS)
     half = torch.full((T, ER), float("nan"), device=gpu)
