@@ -18,6 +18,10 @@ the routing computed live instead of frozen, and the tail fused):
                                 (weight streaming: 5+6 and 7+8 are one launch each,
                                  moe_gemm_shared)
     9. merge + ResAdd           out = bf16(sum_k Y[t, k] + h + s)         block_merge
+                                (T <= 4: 7-9 are one launch, down_token_major:
+                                 out = bf16(sum_k w * (act . w2^T) + shared + h), fp32
+                                 over all experts, one rounding -- the reference's
+                                 token-major strategy #9(b))
 
 At block sizes 64 and 128 (prefill) the four GEMMs read weights packed once in the
 constructor (`pack_w512`: every 32-k stage of a 512-row W tile as 32 KB of contiguous
@@ -38,6 +42,7 @@ from . import _lib
 from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
                        moe_align_block_size_into, route_gateup_shared_into, topk_align_into)
 from .kernels import add_rmsnorm as KN
+from .kernels import moe_down_merge as KD
 from .kernels import norm_router as KR
 from .kernels.moe_gateup import moe_gemm, moe_gemm_packed, moe_gemm_shared, pack_w512
 
@@ -81,7 +86,7 @@ class MoEBlock:
     def __init__(self, T: int, w_norm, wgt, bias, w13, w2, w13s, w2s, block_m: int | None = None,
                  shared_block_m: int | None = None, variant: str | None = None,
                  eps: float = C.RMS_NORM_EPS, scale: float = C.ROUTED_SCALING_FACTOR,
-                 pack: bool = True):
+                 pack: bool = True, token_major: bool | None = None):
         _lib.require_gpu(w_norm, wgt, bias, w13, w2, w13s, w2s)
         dev = w13.device
         self.T = T
@@ -122,6 +127,10 @@ class MoEBlock:
         # weight-streaming decode runs the shared expert inside the routed launches
         self.shared_fused = self.bm == 16
         self.front_fused = T <= DECODE_FRONT_MAX_T and self.shared_fused
+        # decode tail: the token-major down GEMV sums each token's experts, the shared
+        # expert and h in one launch (no Y rows, no merge launch)
+        self.token_major = (self.front_fused and variant is None) if token_major is None \
+            else bool(token_major)
         self.gate_rows = wgt.t().contiguous() if self.decode else None  # [E, H]
         self.wgt_rows = self.gate_rows.t() if self.decode else None  # its [H, E] view
         need = KR.workspace_bytes(T, H, E)
@@ -199,6 +208,15 @@ class MoEBlock:
         self.w13_step()
         self.w2_step()
 
+    def tail(self):
+        """Steps 7-9: the token-major GEMV at decode sizes, else w2 then the merge."""
+        if self.token_major:
+            KD.launch_down_token_major(self.act, self.w2, self.out, self.topw, self.topi, self.h,
+                                       self.topk, {}, True, self.act_s, self.w2s)
+            return
+        self.w2_step()
+        self.merge()
+
     def merge(self):
         y3 = self.ybuf.view(self.T, self.topk, self.H)
         _lib.call("glm52_block_merge", _lib.ptr(y3), y3.stride(0), y3.stride(1),
@@ -209,8 +227,8 @@ class MoEBlock:
         if x.shape != (self.T, self.H) or r.shape != (self.T, self.H):
             raise ValueError(f"expected x, r of shape {(self.T, self.H)}")
         self.front_end(x, r)
-        self.experts()
-        self.merge()
+        self.w13_step()
+        self.tail()
         return self.out
 
     __call__ = forward

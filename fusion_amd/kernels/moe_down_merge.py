@@ -8,9 +8,12 @@
   launch_resadd(x, r, o, cfg): o = bf16(fp32 x + fp32 r)
   launch_seed(o, r, cfg, from_residual): o = r, or zeros
 
-The atomic-merge epilogue (`fuse_merge=True`) and the token-major GEMV are the ranked
-"next" items of this build; they raise NotImplementedError rather than run something
-else.
+  launch_down_token_major(a, w2, out, topk_weights, topk_ids, residual, top_k, cfg,
+                          add_residual): out = bf16(sum_k w * (a . w2^T) (+ residual)),
+      one token per workgroup column slice, fp32 over all experts, one rounding
+
+The atomic-merge epilogue (`fuse_merge=True`) is the ranked "next" item of this build; it
+raises NotImplementedError rather than run something else.
 """
 
 from __future__ import annotations
@@ -38,14 +41,51 @@ def launch_down(a, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
 
 
 def smem_bytes_tokmaj(cfg: dict) -> int:
-    """LDS of the token-major down GEMV (`glm52/kernels/moe_down_merge.py:421-424`), which
-    this build does not implement (see `launch_down_token_major`)."""
-    raise NotImplementedError("token-major down GEMV is not part of this build yet")
+    """LDS of the token-major down GEMV (`glm52/kernels/moe_down_merge.py:421-424`): none,
+    every lane keeps its rows and activation chunks in registers."""
+    return 0
 
 
 def launch_down_token_major(a, w2, out, topk_weights, topk_ids, residual, top_k, cfg,
-                            add_residual: bool):
-    raise NotImplementedError("token-major down GEMV is not part of this build yet")
+                            add_residual: bool, a_shared=None, w2_shared=None):
+    """a: [T*top_k, I].  out: [T, H].  topk_ids/topk_weights: [T, top_k].
+
+    out[t] = bf16(sum_k w[t, k] * (a[t*top_k + k] @ w2[ids[t, k]]^T) (+ residual[t])), one
+    fp32 accumulation, one rounding (`moe_down_merge.py:479-516`).  `a_shared` [T, I] and
+    `w2_shared` [H, I] (this build's extension) add a shared expert with weight 1."""
+    _lib.require_gpu(a, w2, out, topk_weights, topk_ids, residual if add_residual else None,
+                     a_shared, w2_shared)
+    T = topk_ids.shape[0]
+    E, H, K = w2.shape
+    if a.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16 or out.dtype != torch.bfloat16:
+        raise ValueError("token-major operands are bf16")
+    if a.shape[0] < T * top_k or a.shape[1] != K or tuple(out.shape) != (T, H):
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, w2 {tuple(w2.shape)}, "
+                         f"out {tuple(out.shape)}, T={T}, top_k={top_k}")
+    if a.stride(1) != 1 or w2.stride(2) != 1 or out.stride(1) != 1:
+        raise ValueError("a rows, w2 rows and out rows must be contiguous")
+    if topk_ids.dtype != torch.int32:
+        topk_ids = topk_ids.to(torch.int32)
+    if topk_weights.dtype != torch.float32 or topk_weights.stride(1) != 1 \
+            or topk_ids.stride(1) != 1 or topk_ids.stride(0) != topk_weights.stride(0):
+        raise ValueError("topk weights (fp32) and ids (int32) must share a row stride")
+    res = residual if add_residual else None
+    if res is not None and (tuple(res.shape) != (T, H) or res.stride(1) != 1):
+        raise ValueError("residual must be [T, H] with H contiguous")
+    if (a_shared is None) != (w2_shared is None):
+        raise ValueError("a_shared and w2_shared go together")
+    if w2_shared is not None and (tuple(w2_shared.shape[-2:]) != (H, K)
+                                  or a_shared.shape[-1] != K):
+        raise ValueError("shared expert shapes must be [T, I] and [H, I]")
+    ws = w2_shared.reshape(H, K) if w2_shared is not None else None
+    _lib.call(
+        "glm52_down_token_major", _lib.ptr(a), a.stride(0), _lib.ptr(w2), w2.stride(0),
+        w2.stride(1), _lib.ptr(topk_weights), _lib.ptr(topk_ids), topk_ids.stride(0),
+        int(top_k), E, _lib.ptr(a_shared), a_shared.stride(0) if a_shared is not None else 0,
+        _lib.ptr(ws), ws.stride(0) if ws is not None else 0, _lib.ptr(res),
+        res.stride(0) if res is not None else 0, _lib.ptr(out), out.stride(0), T, H, K,
+        _lib.stream(),
+    )
 
 
 def launch_moe_sum(c3, out, residual, topk, cfg, add_residual: bool):

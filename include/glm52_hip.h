@@ -231,6 +231,20 @@ int glm52_router_logits_rstd(const void* y, int64_t stride_y, const void* wgt, i
                              int64_t stride_l, void* workspace, int64_t workspace_bytes, int T,
                              int H, int E, hipStream_t stream);
 
+/* Token-major down GEMV + expert merge (+ residual): fusion #8(b) / #9(b), replaces
+ * moe_down_merge.launch_down_token_major (glm52/kernels/moe_down_merge.py:479-516,
+ * moe_down_token_major_kernel :165-293).
+ *   out[t, n] = bf16(sum_k w[t, k] * (a[t * top_k + k] . w2[ids[t, k], n]) (+ r[t, n])),
+ * fp32 accumulation over all of a token's experts, one rounding, no atomics.  ids outside
+ * [0, num_experts) contribute nothing.  With w2_shared non-null a shared expert (activation
+ * a_shared[t], weight 1) joins the sum.  K (= I) must be 1024 or 2048. */
+int glm52_down_token_major(const void* a, int64_t stride_am, const void* w2, int64_t stride_we,
+                           int64_t stride_wn, const float* topk_weights, const int32_t* topk_ids,
+                           int64_t stride_tk, int top_k, int num_experts, const void* a_shared,
+                           int64_t stride_as, const void* w2_shared, int64_t stride_ws,
+                           const void* residual, int64_t stride_rm, void* out, int64_t stride_om,
+                           int T, int N, int K, hipStream_t stream);
+
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */
 int glm52_silu_and_mul(const void* x, int64_t stride_x, void* y, int64_t stride_y, int M, int I,

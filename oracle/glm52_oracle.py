@@ -31,6 +31,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   moe_sum / merge_resadd     closed forms (weighted sums) on small shapes
   oproj_gemm / oproj_cast    one-hot A (exact rows of B, with and without the residual);
                              fp64 textbook GEMM on small shapes
+  down_token_major           single expert with w = 1 equals the fp64 GEMM row; linearity
+                             in the weights; closed forms on one-hot rows; within one
+                             bf16 rounding per expert of moe_sum over the unfused rows
   rstd_exact                 exact rational sum of squares; constant rows (closed form);
                              exact halving under h -> 2h at eps = 0; rmsnorm_exact's y
   fold_weight                power-of-two w (exact), w = 1 (identity), axis choice
@@ -289,6 +292,30 @@ def merge_resadd(y3, wt, res, round_mid: bool = True) -> torch.Tensor:
     if round_mid:
         acc = acc.to(y3.dtype).float()
     return (acc + res.float()).to(y3.dtype)
+
+
+# --------------------------------------------------------------------------------------
+# token-major down GEMV (fusion #8(b) / #9(b))
+# --------------------------------------------------------------------------------------
+def down_token_major(a, w2, topk_weights, topk_ids, residual=None, a_shared=None,
+                     w2_shared=None) -> torch.Tensor:
+    """`moe_down_token_major_kernel` (`glm52/kernels/moe_down_merge.py:165-293`): for each
+    token t, sum_k w[t, k] * (a[t * top_k + k] @ w2[ids[t, k]]^T) accumulated without
+    rounding (here fp64, rounded once to fp32), plus the shared expert's product with
+    weight 1 if given, then + fp32 residual and one rounding to bf16.  [T, H] bf16."""
+    T, k = topk_ids.shape
+    acc = torch.zeros(T, w2.shape[1], dtype=torch.float64)
+    ad = a.double()
+    for t in range(T):
+        for j in range(k):
+            e = int(topk_ids[t, j])
+            acc[t] += float(topk_weights[t, j]) * (w2[e].double() @ ad[t * k + j])
+        if w2_shared is not None:
+            acc[t] += w2_shared.reshape(w2.shape[1], -1).double() @ a_shared[t].double()
+    v = acc.float()
+    if residual is not None:
+        v = v + residual.float()
+    return v.to(BF16)
 
 
 # --------------------------------------------------------------------------------------

@@ -482,3 +482,66 @@ def test_prenorm_gateup_rows_one_hot_and_identity():
     x2 = O.rmsnorm_exact(h, wn)
     un = O.prenorm_gateup_rows(x2, w13, np.ones(T, dtype=np.float32), ids)
     assert O.rel_err(got, un) < 5e-2
+
+
+# ------------------------------------------------------------------ token-major down GEMV
+def _tokmaj_problem(T=3, k=2, E=4, H=24, K=32, seed=31):
+    g = torch.Generator().manual_seed(seed)
+    a = (torch.randn(T * k, K, generator=g) * 0.5).to(BF16)
+    w2 = (torch.randn(E, H, K, generator=g) * 0.1).to(BF16)
+    ids = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    tw = torch.rand(T, k, generator=g) + 0.25
+    return a, w2, ids, tw
+
+
+def test_down_token_major_rational_and_closed_forms():
+    a, w2, ids, tw = _tokmaj_problem()
+    T, k = ids.shape
+    out = O.down_token_major(a, w2, tw, ids)
+    # exact rational sums of the weighted products, rounded once (fp32, then bf16)
+    for t in range(T):
+        for n in (0, 7, 23):
+            s = sum(Fraction(float(tw[t, j])) * sum(Fraction(float(a[t * k + j, q])) *
+                                                    Fraction(float(w2[int(ids[t, j]), n, q]))
+                                                    for q in range(a.shape[1]))
+                    for j in range(k))
+            want = torch.tensor(np.float32(float(s))).to(BF16)
+            assert torch.equal(out[t, n], want)
+    # one-hot rows with weight 1: the output row is the sum of the selected W columns
+    a1 = torch.zeros_like(a)
+    a1[:, 5] = 1.0
+    ones = torch.ones_like(tw)
+    got = O.down_token_major(a1, w2, ones, ids)
+    for t in range(T):
+        col = sum(w2[int(ids[t, j]), :, 5].double() for j in range(k))
+        assert torch.equal(got[t], col.float().to(BF16))
+    # linearity: doubling the weights doubles the output exactly (no residual)
+    assert torch.equal(O.down_token_major(a, w2, tw * 2, ids).float(), out.float() * 2)
+
+
+def test_down_token_major_shared_and_residual_and_unfused():
+    a, w2, ids, tw = _tokmaj_problem(seed=32)
+    T, k = ids.shape
+    H, K = w2.shape[1:]
+    g = torch.Generator().manual_seed(33)
+    a_s = (torch.randn(T, K, generator=g) * 0.5).to(BF16)
+    w2_s = (torch.randn(1, H, K, generator=g) * 0.1).to(BF16)
+    r = torch.randn(T, H, generator=g).to(BF16)
+    got = O.down_token_major(a, w2, tw, ids, r, a_s, w2_s)
+    routed = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        for j in range(k):
+            routed[t] += float(tw[t, j]) * (w2[int(ids[t, j])].double() @ a[t * k + j].double())
+    shared = a_s.double() @ w2_s[0].double().t()
+    want = ((routed + shared).float() + r.float()).to(BF16)
+    assert torch.equal(got, want)
+    # the unfused chain rounds every expert's row to bf16 first (moe_sum over Y)
+    y3 = torch.empty(T, k, H, dtype=BF16)
+    for t in range(T):
+        for j in range(k):
+            acc = (w2[int(ids[t, j])].double() @ a[t * k + j].double()).float()
+            y3[t, j] = (acc * float(tw[t, j])).to(BF16)
+    un = O.moe_sum(y3, None)
+    fused = O.down_token_major(a, w2, tw, ids)
+    bound = (k + 1) * 2.0 ** -8 * y3.float().abs().sum(dim=1) + 1e-6
+    assert ((un.float() - fused.float()).abs() <= bound).all()
