@@ -175,6 +175,7 @@ def main() -> int:
             "bias": bias,
         }
         if not args.no_oproj:
+            rec["down_merge"] = down_merge_bench(blk, W, T, n_e, timed, args.steps, args.warmup)
             rec["oproj"] = oproj_bench(T, timed, args.steps, args.warmup, dev)
             rec["prenorm_router"] = prenorm_bench(T, timed, args.steps, args.warmup, dev)
         per_T[str(T)] = rec
@@ -321,6 +322,59 @@ def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
             "roofline_frac": round(roof / us, 4), "bound": kc.bound(),
             "GBps": round(kc.bytes / (us * 1e-6) / 1e9, 1),
             "TFLOPs": round(kc.flops / (us * 1e-6) / 1e12, 1)}
+
+
+def down_merge_bench(blk, W, T: int, n_e: int, timed, steps: int, warmup: int) -> dict:
+    """The reference's three accumulation strategies for the routed down GEMM + merge +
+    residual (fusions #8 / #9, `glm52/bench/bench_f08f09_down_merge_resadd.py:1-30`), on
+    the block's own activations and routing at this T with the real w2 (routed experts
+    only, residual = h): unfused = down GEMM into [T, 8, H] then moe_sum with the residual;
+    atomic = seed out with the residual, then the GEMM adding into it (`fuse_merge=True`);
+    token-major = one launch summing each token's experts (T <= 256 only: above, every
+    token re-streams its experts).  The roofline counts w2 once per distinct expert, the
+    activation rows, the residual and the output (the unfused chain's [T, 8, H] round trip
+    is its own cost, not the roofline's)."""
+    import torch
+
+    from fusion_amd import roofline as RL
+    from fusion_amd.kernels import moe_down_merge as KD
+
+    H, I, k = blk.H, blk.I, blk.topk
+    R = T * k
+    cfg = {"BLOCK_M": blk.bm}
+    if getattr(blk, "packed", False):
+        cfg["w2_packed"] = blk.w2_p
+    tw = blk.topw.reshape(-1)
+    c3 = torch.empty(R, H, dtype=torch.bfloat16, device=blk.h.device)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=blk.h.device)
+
+    def unfused():
+        KD.launch_down(blk.act, W.w2, c3, tw, blk.sti, blk.eids, blk.ntp, R, k, cfg, False)
+        KD.launch_moe_sum(c3, out, blk.h, k, {}, True)
+
+    def atomic():
+        KD.launch_seed(out, blk.h, {}, True)
+        KD.launch_down(blk.act, W.w2, out, tw, blk.sti, blk.eids, blk.ntp, R, k, cfg, True)
+
+    def token_major():
+        KD.launch_down_token_major(blk.act, W.w2, out, blk.topw, blk.topi, blk.h, k, {}, True)
+
+    res = {}
+    for name, fn in (("unfused_us", unfused), ("atomic_us", atomic),
+                     ("token_major_us", token_major if T <= 256 else None)):
+        if fn is None:
+            res[name] = None
+            continue
+        ms, _ = timed(fn, steps, warmup)
+        res[name] = round(statistics.median(ms) * 1e3, 2)
+    kc = RL.KernelCost("down_merge", 2.0 * R * I * H,
+                       n_e * H * I * 2 + R * I * 2 + 2 * T * H * 2)
+    roof = kc.seconds() * 1e6
+    best = min(v for v in res.values() if v is not None)
+    res.update({"roofline_us": round(roof, 2), "roofline_frac": round(roof / best, 4),
+                "bound": kc.bound()})
+    del c3, out
+    return res
 
 
 def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:

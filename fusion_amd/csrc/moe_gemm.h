@@ -138,7 +138,20 @@ struct GemmArgs {
   const uint16_t* R;
   int64_t srm;
   float* C32;
+  // > 0: the atomic expert merge (FUSE_MERGE): the bf16 result of flat token f is added
+  // with packed bf16 atomics into row f / merge_topk of C (non-gated only; the 512-row
+  // tile and contiguous-run mappings); 0: the result is stored into row f
+  int merge_topk;
 };
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+// C[0..1] += (lo, hi) as one packed bf16 atomic (global_atomic_pk_add_bf16); p 4-byte
+// aligned.  Each element's add rounds to bf16, in whatever order the adds land.
+GLM52_DEV void atomic_add_bf16x2(uint16_t* p, float lo, float hi) {
+  __builtin_amdgcn_global_atomic_fadd_v2bf16(reinterpret_cast<bf16x2_t*>(p),
+                                             __builtin_bit_cast(bf16x2_t, pack_bf16x2(lo, hi)));
+}
 
 // The wide LDS-tiled mapping fed by direct global -> LDS loads (moe_gemm_wide.hip):
 // returns GLM52_EUNSUPPORTED for a block size or shape it has no instance for.

@@ -452,6 +452,46 @@ extern "C" int glm52_pack_w512(const void* w, int64_t stride_we, int64_t stride_
   return rc < 0 ? (int)(-rc) : GLM52_OK;
 }
 
+// The down GEMM with the atomic expert merge (FUSE_MERGE): for every valid flat token f of
+// the layout, out[f / top_k, :] += bf16(topk_weights[f] * (a[f] . w[e]^T)), each add a
+// packed bf16 atomic (two outputs a word), so the order of a row's adds -- and with it the
+// rounding -- depends on timing.  out [T, n_out] must be seeded by the caller (zeros, or
+// the residual).  w_packed (glm52_pack_w512 of w, may be null) is read by the 512-row tile
+// mapping.  block_m 16 (contiguous-run mapping) or 64 / 128 (512-row tiles).
+extern "C" int glm52_moe_down_merge(const void* a, int64_t stride_am, const void* w,
+                                    int64_t stride_we, int64_t stride_wn, const void* w_packed,
+                                    void* out, int64_t stride_om, const float* topk_weights,
+                                    const int32_t* sorted_token_ids, const int32_t* expert_ids,
+                                    const int32_t* num_tokens_post_padded, int capacity,
+                                    int block_m, int num_valid_tokens, int top_k, int n_out,
+                                    int k, hipStream_t stream) {
+  if (!a || !w || !out || !topk_weights || !sorted_token_ids || !expert_ids ||
+      !num_tokens_post_padded || top_k < 1)
+    return GLM52_EINVAL;
+  if (capacity < 0 || (capacity % 16) != 0 || n_out <= 0 || (n_out % 16) || k <= 0 || (k % 256))
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w) || (stride_am % 8) || (stride_we % 8) || (stride_wn % 8) ||
+      (reinterpret_cast<uintptr_t>(out) & 3u) || (stride_om % 2) || stride_om < n_out ||
+      (w_packed && !al16(w_packed)))
+    return GLM52_EINVAL;
+  if (block_m != 16 && block_m != 64 && block_m != 128) return GLM52_EUNSUPPORTED;
+  if (capacity % block_m) return GLM52_EINVAL;
+  if (capacity == 0) return GLM52_OK;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, 1, static_cast<const uint16_t*>(w),
+             stride_we, stride_wn, 0, static_cast<uint16_t*>(out), stride_om, topk_weights,
+             sorted_token_ids, expert_ids, num_tokens_post_padded, block_m, n_out, k,
+             num_valid_tokens, 4, 64, nullptr, 0, nullptr, nullptr, 0, 0,
+             a_bytes(num_valid_tokens, 1, stride_am, k), 0};
+  g.merge_topk = top_k;
+  if (block_m == 16) {
+    if (w_packed) return GLM52_EINVAL;  // the run mapping reads w in place
+    return launch_runs(g, capacity, false, true, false, stream);
+  }
+  if (g.a_bytes >= 0x7ffffff0) return GLM52_EUNSUPPORTED;
+  g.Wp = static_cast<const uint16_t*>(w_packed);
+  return launch_wide512(g, capacity, false, true, stream);
+}
+
 extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row_div,
                                      const void* w_packed, void* c, int64_t stride_cm,
                                      const float* topk_weights,

@@ -428,6 +428,15 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     const int slot = (it / (int)gridDim.x) % NMETA;
     const int c = wv * 4 + lane / 16;  // token column of the slice
     const int j = lane % 16;           // output of the item
+    if (!GATED && p.merge_topk > 0) {  // atomic merge: lane pairs (j, j + 1) add as one word
+      const int tok = meta_tok[slot][c];
+      float v = rsum(par, j, c);
+      if (WEIGHTED && !extra) v = v * meta_w[slot][c];
+      const float v1 = __shfl_down(v, 1, 16);  // every lane is active here
+      if (tok < 0 || (j & 1) || extra) return;
+      atomic_add_bf16x2(p.C + (int64_t)(tok / p.merge_topk) * p.scm + n0 + j, v, v1);
+      return;
+    }
     if (GATED && j >= 8) return;
     const int tok = meta_tok[slot][c];
     if (tok < 0) return;

@@ -347,6 +347,8 @@ GLM52_DEV int w512_row(bool gated, int gu_rel, int w, int i, int l) {
 }
 GLM52_DEV int w512_chunk(int l) { return (l & 3) ^ (((l >> 2) >> 2) & 3); }
 
+// EPI (non-gated): 0 bf16 store; 1 bf16(acc + R); 2 C32 += acc (+ R); 3 C32 = acc (fp32
+// partials); 4 the atomic expert merge, bf16 packed atomic adds into row tok / merge_topk.
 template <int MT, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   constexpr int NTW = 512;         // W rows per tile
@@ -522,7 +524,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       for (int t = 0; t < NV; ++t) {
         const int tok = p.sti[row0 + t * 32 + l32];
         if (tok >= p.num_valid) continue;
-        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;
+        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;  // EPI 0, 1
         if (GATED) {
 #pragma unroll
           for (int fp = 0; fp < 2; ++fp) {
@@ -566,6 +568,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            } else if (EPI == 4) {  // atomic merge into row tok / top_k, two outputs a word
+              uint16_t* dst = p.C + (int64_t)(tok / p.merge_topk) * p.scm + col;
+#pragma unroll
+              for (int q = 0; q < 8; ++q) atomic_add_bf16x2(dst + 2 * q, v[2 * q], v[2 * q + 1]);
             } else {
               uint16_t* dst = crow + col;
               *reinterpret_cast<uint4*>(dst) = pack8(v);
@@ -608,6 +614,17 @@ int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
     }
   } else {
     if (a.epi != 0) return GLM52_EUNSUPPORTED;
+  }
+  if (a.merge_topk > 0) {  // the atomic expert merge: weighted w2 only
+    if constexpr (!GATED && WEIGHTED) {
+      if (a.Wp)
+        moe_gemm_w512_kernel<MT, false, true, true, 4><<<grid, 256, 0, st>>>(a);
+      else
+        moe_gemm_w512_kernel<MT, false, true, false, 4><<<grid, 256, 0, st>>>(a);
+      GLM52_RETURN_LAUNCH();
+    } else {
+      return GLM52_EUNSUPPORTED;
+    }
   }
   if (a.Wp)
     moe_gemm_w512_kernel<MT, GATED, WEIGHTED, true><<<grid, 256, 0, st>>>(a);

@@ -8,12 +8,12 @@
   launch_resadd(x, r, o, cfg): o = bf16(fp32 x + fp32 r)
   launch_seed(o, r, cfg, from_residual): o = r, or zeros
 
+  launch_down(..., fuse_merge=True): c[f // top_k, :] += bf16(topk_w[f] * (a[f] . w2[e]^T))
+      with packed bf16 atomics into the pre-seeded [T, H] output (strategy (a))
   launch_down_token_major(a, w2, out, topk_weights, topk_ids, residual, top_k, cfg,
                           add_residual): out = bf16(sum_k w * (a . w2^T) (+ residual)),
       one token per workgroup column slice, fp32 over all experts, one rounding
-
-The atomic-merge epilogue (`fuse_merge=True`) is the ranked "next" item of this build; it
-raises NotImplementedError rather than run something else.
+      (strategy (b))
 """
 
 from __future__ import annotations
@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 
 from .. import _lib
-from .moe_gateup import moe_gemm
+from .moe_gateup import check_layout, moe_gemm
 
 
 def smem_bytes(cfg: dict) -> int:
@@ -33,11 +33,36 @@ def smem_bytes(cfg: dict) -> int:
 
 def launch_down(a, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
                 num_tokens_post_padded, num_valid_tokens, top_k, cfg, fuse_merge: bool):
-    """a: [rows, I] bf16.  w2: [E, H, I] bf16.  c: [rows, H] (fuse_merge=False)."""
-    if fuse_merge:
-        raise NotImplementedError("atomic FUSE_MERGE epilogue is not part of this build yet")
-    moe_gemm(a, 1, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
-             num_tokens_post_padded, num_valid_tokens, w2.shape[1], 0, False, cfg)
+    """a: [rows, I] bf16.  w2: [E, H, I] bf16.
+    c: [rows, H] when fuse_merge=False, else the pre-seeded [T, H] output, to which every
+    routed row's bf16 result is added with packed bf16 atomics (`moe_down_merge.py:
+    160-169`); `cfg["w2_packed"]` (`moe_gateup.pack_w512(w2, H, 0, False)`) may supply
+    the packed weights the 64/128-row mapping reads."""
+    if not fuse_merge:
+        moe_gemm(a, 1, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
+                 num_tokens_post_padded, num_valid_tokens, w2.shape[1], 0, False, cfg)
+        return
+    wp = cfg.get("w2_packed")
+    _lib.require_gpu(a, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
+                     num_tokens_post_padded, wp)
+    if a.dtype != torch.bfloat16 or w2.dtype != torch.bfloat16 or c.dtype != torch.bfloat16:
+        raise ValueError("down GEMM operands are bf16")
+    if a.stride(1) != 1 or w2.stride(2) != 1 or c.stride(1) != 1:
+        raise ValueError("a rows, w2 rows and c rows must be contiguous")
+    if topk_weights_flat.dtype != torch.float32 or not topk_weights_flat.is_contiguous():
+        raise ValueError("topk weights must be a contiguous fp32 tensor")
+    H, K = w2.shape[1], w2.shape[2]
+    if a.shape[1] != K or c.shape[1] != H or c.shape[0] * top_k < num_valid_tokens:
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, w2 {tuple(w2.shape)}, "
+                         f"c {tuple(c.shape)} (the merged [T, H] output), top_k={top_k}")
+    bm = int(cfg["BLOCK_M"])
+    cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    _lib.call(
+        "glm52_moe_down_merge", _lib.ptr(a), a.stride(0), _lib.ptr(w2), w2.stride(0),
+        w2.stride(1), _lib.ptr(wp), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights_flat),
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded),
+        cap, bm, int(num_valid_tokens), int(top_k), H, K, _lib.stream(),
+    )
 
 
 def smem_bytes_tokmaj(cfg: dict) -> int:

@@ -231,6 +231,20 @@ int glm52_router_logits_rstd(const void* y, int64_t stride_y, const void* wgt, i
                              int64_t stride_l, void* workspace, int64_t workspace_bytes, int T,
                              int H, int E, hipStream_t stream);
 
+/* The down GEMM with the atomic expert merge: fusion #8(a) / #9(a), replaces
+ * moe_down_merge.launch_down(fuse_merge=True) (glm52/kernels/moe_down_merge.py:427-476,
+ * FUSE_MERGE epilogue :160-169).  For every valid flat token f of the layout,
+ * out[f / top_k, :] += bf16(topk_weights[f] * (a[f] . w[e]^T)), each add a packed bf16
+ * atomic, so the rounding order depends on timing.  out [T, n_out] is seeded by the
+ * caller (zeros or the residual; launch_seed).  block_m 16, 64 or 128; w_packed
+ * (glm52_pack_w512, may be null; not with block_m 16) is read by the 64/128 mapping. */
+int glm52_moe_down_merge(const void* a, int64_t stride_am, const void* w, int64_t stride_we,
+                         int64_t stride_wn, const void* w_packed, void* out, int64_t stride_om,
+                         const float* topk_weights, const int32_t* sorted_token_ids,
+                         const int32_t* expert_ids, const int32_t* num_tokens_post_padded,
+                         int capacity, int block_m, int num_valid_tokens, int top_k, int n_out,
+                         int k, hipStream_t stream);
+
 /* Token-major down GEMV + expert merge (+ residual): fusion #8(b) / #9(b), replaces
  * moe_down_merge.launch_down_token_major (glm52/kernels/moe_down_merge.py:479-516,
  * moe_down_token_major_kernel :165-293).

@@ -34,6 +34,9 @@ Parity status of each function (how it is pinned, see tests/test_oracle.py):
   down_token_major           single expert with w = 1 equals the fp64 GEMM row; linearity
                              in the weights; closed forms on one-hot rows; within one
                              bf16 rounding per expert of moe_sum over the unfused rows
+  down_merge_atomic          top_k = 1 is one rounding of seed + bf16(y) (closed form);
+                             integer-valued sums are exact in any order; within one
+                             rounding per add of down_token_major
   rstd_exact                 exact rational sum of squares; constant rows (closed form);
                              exact halving under h -> 2h at eps = 0; rmsnorm_exact's y
   fold_weight                power-of-two w (exact), w = 1 (identity), axis choice
@@ -316,6 +319,23 @@ def down_token_major(a, w2, topk_weights, topk_ids, residual=None, a_shared=None
     if residual is not None:
         v = v + residual.float()
     return v.to(BF16)
+
+
+def down_merge_atomic(a, w2, topk_weights, topk_ids, seed) -> torch.Tensor:
+    """`moe_down_kernel` with FUSE_MERGE (`glm52/kernels/moe_down_merge.py:154-166`): each
+    routed row's result y = bf16(w * fp32(a[f] @ w2[e]^T)) is added to the seeded output
+    row f // top_k, every add rounded to bf16 (the bf16 `tl.atomic_add`).  The device adds
+    in whatever order the atomics land; this restatement adds in k order, which fixes the
+    value whenever the sums are exact (or top_k = 1).  [T, H] bf16."""
+    T, k = topk_ids.shape
+    out = seed.clone().to(BF16)
+    for t in range(T):
+        for j in range(k):
+            e = int(topk_ids[t, j])
+            acc = (w2[e].double() @ a[t * k + j].double()).float()
+            y = (acc * float(topk_weights[t, j])).to(BF16)
+            out[t] = (out[t].float() + y.float()).to(BF16)
+    return out
 
 
 # --------------------------------------------------------------------------------------

@@ -545,3 +545,35 @@ def test_down_token_major_shared_and_residual_and_unfused():
     fused = O.down_token_major(a, w2, tw, ids)
     bound = (k + 1) * 2.0 ** -8 * y3.float().abs().sum(dim=1) + 1e-6
     assert ((un.float() - fused.float()).abs() <= bound).all()
+
+
+# ------------------------------------------------------------------ atomic expert merge
+def test_down_merge_atomic_closed_forms():
+    a, w2, ids, tw = _tokmaj_problem(T=4, k=1, seed=41)
+    g = torch.Generator().manual_seed(42)
+    seed = torch.randn(4, w2.shape[1], generator=g).to(BF16)
+    got = O.down_merge_atomic(a, w2, tw, ids, seed)
+    for t in range(4):  # top_k = 1: one rounding of seed + bf16(y)
+        y = ((w2[int(ids[t, 0])].double() @ a[t].double()).float() * float(tw[t, 0])).to(BF16)
+        assert torch.equal(got[t], (seed[t].float() + y.float()).to(BF16))
+    # integer-valued rows: every partial sum is exact, so any add order gives the sum
+    T, k, E, H, K = 3, 4, 6, 16, 64
+    a_i = torch.zeros(T * k, K, dtype=BF16)
+    a_i[:, :3] = 1.0
+    w_i = torch.randint(-2, 3, (E, H, K), generator=g).to(BF16)
+    ids_i = torch.stack([torch.randperm(E, generator=g)[:k] for _ in range(T)]).to(torch.int32)
+    tw_i = torch.full((T, k), 2.0)
+    seed_i = torch.randint(-5, 6, (T, H), generator=g).to(BF16)
+    got_i = O.down_merge_atomic(a_i, w_i, tw_i, ids_i, seed_i)
+    want = seed_i.double().clone()
+    for t in range(T):
+        for j in range(k):
+            want[t] += 2.0 * w_i[int(ids_i[t, j]), :, :3].double().sum(-1)
+    assert torch.equal(got_i.double(), want)
+    # against the one-rounding token-major result: within one rounding per add
+    a, w2, ids, tw = _tokmaj_problem(T=3, k=4, seed=43)
+    r = torch.randn(3, w2.shape[1], generator=g).to(BF16)
+    at = O.down_merge_atomic(a, w2, tw, ids, r)
+    tm = O.down_token_major(a, w2, tw, ids, r)
+    bound = 5 * 2.0 ** -8 * (at.float().abs() + 4 * r.float().abs().max()) + 1e-3
+    assert ((at.float() - tm.float()).abs() <= bound).all()
