@@ -320,7 +320,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 int choose_ks(int T, int H) {
   const int tblocks = (T + TB - 1) / TB;
   int ks = 1;
-  while (tblocks * ks < 256 && ks < 32 && (H % (KC * ks * 2)) == 0) ks *= 2;
+  while (tblocks * ks < 512 && ks < 32 && (H % (KC * ks * 2)) == 0) ks *= 2;
   return ks;
 }
 
