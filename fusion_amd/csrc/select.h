@@ -272,10 +272,17 @@ GLM52_DEV void align_body_waves(const int32_t* __restrict__ ids, int numel, int 
   for (int q = tid; q < NW * kMaxE; q += NT) (&sh.wcnt[0][0])[q] = 0;
   __syncthreads();
 
-  // 1. per-wave histograms
-  for (int i = lo + lane; i < hi; i += kWave) {
-    const int e = ids[i];
-    if (e >= 0 && e < E) atomicAdd(&sh.wcnt[wid][e], 1);
+  // 1. per-wave histograms; eight loads of a lane in flight before its first atomic
+  for (int i0 = lo; i0 < hi; i0 += 8 * kWave) {
+    int ev[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + u * kWave + lane;
+      ev[u] = i < hi ? ids[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (ev[u] >= 0 && ev[u] < E) atomicAdd(&sh.wcnt[wid][ev[u]], 1);
   }
   __syncthreads();
 
@@ -333,26 +340,38 @@ GLM52_DEV void align_body_waves(const int32_t* __restrict__ ids, int numel, int 
   if (tid == 0) ntp_out[0] = total;
   __syncthreads();
 
-  // 4. stable scatter, every wave over its own range in index order
-  for (int base = lo; base < hi; base += kWave) {
-    const int i = base + lane;
-    int e = i < hi ? ids[i] : -1;
-    const bool valid = e >= 0 && e < E;
-    if (!valid) e = -1;
-    uint64_t m = __ballot(valid);
+  // 4. stable scatter, every wave over its own range in index order, 64 ids a step; the
+  //    ids of eight steps are loaded before the first of them is ranked
+  for (int b0 = lo; b0 < hi; b0 += 8 * kWave) {
+    int ev[8];
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      const bool bit = valid && ((e >> b) & 1);
-      const uint64_t bm = __ballot(bit);
-      m &= bit ? bm : ~bm;
+    for (int u = 0; u < 8; ++u) {
+      const int i = b0 + u * kWave + lane;
+      ev[u] = i < hi ? ids[i] : -1;
     }
-    const int rank = __popcll(m & lt_mask);
-    int pos = 0;
-    if (valid) {
-      pos = sh.wcnt[wid][e] + rank;
-      sorted_ids[pos] = i;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int base = b0 + u * kWave;
+      if (base >= hi) break;  // wave-uniform
+      const int i = base + lane;
+      int e = ev[u];
+      const bool valid = e >= 0 && e < E;
+      if (!valid) e = -1;
+      uint64_t m = __ballot(valid);
+#pragma unroll
+      for (int b = 0; b < 8; ++b) {
+        const bool bit = valid && ((e >> b) & 1);
+        const uint64_t bm = __ballot(bit);
+        m &= bit ? bm : ~bm;
+      }
+      const int rank = __popcll(m & lt_mask);
+      int pos = 0;
+      if (valid) {
+        pos = sh.wcnt[wid][e] + rank;
+        sorted_ids[pos] = i;
+      }
+      if (valid && rank == 0) sh.wcnt[wid][e] += __popcll(m);  // after every lane's read
     }
-    if (valid && rank == 0) sh.wcnt[wid][e] += __popcll(m);  // after every lane's read
   }
 }
 
