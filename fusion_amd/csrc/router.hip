@@ -316,7 +316,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   }
 }
 
-// K split for T tokens: enough workgroups to cover the chip at small T.
+// K split for T tokens: enough workgroups for two per CU (512), at most 32 slices.
 int choose_ks(int T, int H) {
   const int tblocks = (T + TB - 1) / TB;
   int ks = 1;

@@ -26,8 +26,10 @@ def test_header_declares_every_binding():
 def test_router_workspace_query():
     from fusion_amd.kernels import norm_router as KR
 
+    # K is split until 512 workgroups (two per CU) run, at most 32 ways
     assert KR.workspace_bytes(1) > 0  # decode splits K
-    assert KR.workspace_bytes(8192) == 0  # prefill covers the chip without a split
+    assert KR.workspace_bytes(8192) == 2 * 8192 * 256 * 8  # 256 token blocks x 2 K slices
+    assert KR.workspace_bytes(16384) == 0  # 512 token blocks: no split
     assert KR.workspace_bytes(256) == 32 * 256 * 256 * 8  # 8 token blocks x 32 K slices
 
 
