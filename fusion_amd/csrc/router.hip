@@ -18,8 +18,8 @@
 // CPU oracle applies the same rule, so ids agree bit for bit.
 //
 // Two mappings, picked by the gate's layout.  Rows ([E, H], K contiguous, used at small
-// T): a wave per expert streams its row once (`router_rows_kernel`).  Columns ([H, E],
-// the reference kernel's layout): the logits run on the fp64 matrix cores
+// T): a workgroup per expert row and group of 4 tokens (`router_rows_kernel`).  Columns
+// ([H, E], the reference kernel's layout): the logits run on the fp64 matrix cores
 // (`v_mfma_f64_16x16x4_f64`), a workgroup per 32 tokens x all experts of a K slice, gate
 // and token chunks staged through two LDS buffers (`router_logits_kernel`).  Small T
 // splits K over KS workgroups; their fp64 partials land in a caller-provided workspace
@@ -184,62 +184,86 @@ __global__ __launch_bounds__(256) void router_logits_kernel(
   }
 }
 
-// Row layout (gate as [E, H], rows contiguous), for small T: a wave per expert streams
-// its 12 KB gate row once, each lane 8 consecutive k per step with 16-byte loads, and
-// dots it with the T <= RT token rows staged in LDS; the fp64 lane sums meet in a fixed
-// butterfly.  grid = (ceil(E / 4), ceil(T / RT)); block = 256.
+// Row layout (gate as [E, H], rows contiguous), for small T: a workgroup per (gate row e,
+// group of RT tokens).  Thread (w, l) owns the 16-byte chunks w * H/32 + l + 64 j of the
+// gate row and of each token row (a wave takes a quarter of the row), and issues all of
+// its loads before its first FMA, so a workgroup waits for one round of memory latency.
+// fp64 FMAs; each token's four wave sums meet in wave order.
+// grid = (E, ceil(T / RT)); block = 256.
 constexpr int RT = 4;
 constexpr int HMAX = 8192;
+constexpr int RNJ = HMAX / 32 / kWave;  // chunks per lane of a quarter row (H <= HMAX)
 
 template <bool WG_F32>
 __global__ __launch_bounds__(256) void router_rows_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const void* __restrict__ wg_raw, int64_t swe,
     float* __restrict__ logits, int64_t sl, int T, int H, int E, const float* __restrict__ rstd) {
-  extern __shared__ __attribute__((aligned(16))) uint16_t ys[];  // [min(RT, T - t0)][H]
+  __shared__ double part[RT][4];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
-  const int e = blockIdx.x * 4 + tid / kWave;
+  const int wv = tid / kWave;
+  const int e = blockIdx.x;
   const int t0 = blockIdx.y * RT;
   const int nt = min(RT, T - t0);
-  const int nch = H / 8;
-  for (int q = tid; q < nt * nch; q += 256) {
-    const int t = q / nch, c = q % nch;
-    *reinterpret_cast<uint4*>(&ys[t * H + c * 8]) =
-        *reinterpret_cast<const uint4*>(y + (int64_t)(t0 + t) * sy + c * 8);
-  }
-  __syncthreads();
-  if (e >= E) return;
-  double acc[RT];
+  const int qc = H / 32;
+  uint4 yr[RT][RNJ];
 #pragma unroll
-  for (int t = 0; t < RT; ++t) acc[t] = 0.0;
-  for (int c = lane; c < nch; c += kWave) {
-    float wf[8];
-    if constexpr (WG_F32) {
-      const float* wr = static_cast<const float*>(wg_raw) + (int64_t)e * swe + c * 8;
-      const float4 a = *reinterpret_cast<const float4*>(wr);
-      const float4 b = *reinterpret_cast<const float4*>(wr + 4);
-      wf[0] = a.x; wf[1] = a.y; wf[2] = a.z; wf[3] = a.w;
-      wf[4] = b.x; wf[5] = b.y; wf[6] = b.z; wf[7] = b.w;
-    } else {
-      unpack8(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(wg_raw) +
-                                              (int64_t)e * swe + c * 8), wf);
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int j = 0; j < RNJ; ++j) {
+      const int c = wv * qc + lane + kWave * j;
+      const bool ok = t < nt && lane + kWave * j < qc;
+      yr[t][j] = ok ? *reinterpret_cast<const uint4*>(y + (int64_t)(t0 + t) * sy + c * 8)
+                    : make_uint4(0, 0, 0, 0);
+    }
+  float wf[RNJ][8];
+  if constexpr (WG_F32) {
+    float4 g0[RNJ], g1[RNJ];
+    const float* wr = static_cast<const float*>(wg_raw) + (int64_t)e * swe;
+#pragma unroll
+    for (int j = 0; j < RNJ; ++j) {
+      const int c = wv * qc + lane + kWave * j;
+      const bool ok = lane + kWave * j < qc;
+      g0[j] = ok ? *reinterpret_cast<const float4*>(wr + c * 8) : make_float4(0.f, 0.f, 0.f, 0.f);
+      g1[j] = ok ? *reinterpret_cast<const float4*>(wr + c * 8 + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
 #pragma unroll
-    for (int t = 0; t < RT; ++t) {
-      if (t < nt) {
-        float yf[8];
-        unpack8(*reinterpret_cast<const uint4*>(&ys[t * H + c * 8]), yf);
-#pragma unroll
-        for (int q = 0; q < 8; ++q) acc[t] = fma((double)yf[q], (double)wf[q], acc[t]);
-      }
+    for (int j = 0; j < RNJ; ++j) {
+      wf[j][0] = g0[j].x; wf[j][1] = g0[j].y; wf[j][2] = g0[j].z; wf[j][3] = g0[j].w;
+      wf[j][4] = g1[j].x; wf[j][5] = g1[j].y; wf[j][6] = g1[j].z; wf[j][7] = g1[j].w;
     }
+  } else {
+    uint4 gr[RNJ];
+    const uint16_t* wr = static_cast<const uint16_t*>(wg_raw) + (int64_t)e * swe;
+#pragma unroll
+    for (int j = 0; j < RNJ; ++j) {
+      const int c = wv * qc + lane + kWave * j;
+      gr[j] = lane + kWave * j < qc ? *reinterpret_cast<const uint4*>(wr + c * 8)
+                                    : make_uint4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < RNJ; ++j) unpack8(gr[j], wf[j]);
   }
 #pragma unroll
   for (int t = 0; t < RT; ++t) {
     if (t < nt) {  // each reduction is 12 cross-lane moves: only the tokens that exist
-      const double s = wave_sum_f64(acc[t]);
-      if (lane == 0) logits[(int64_t)(t0 + t) * sl + e] = rstd ? (float)s * rstd[t0 + t] : (float)s;
+      double acc = 0.0;
+#pragma unroll
+      for (int j = 0; j < RNJ; ++j) {
+        float yf[8];
+        unpack8(yr[t][j], yf);  // chunks past the row are zero
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc = fma((double)yf[q], (double)wf[j][q], acc);
+      }
+      acc = wave_sum_f64(acc);
+      if (lane == 0) part[t][wv] = acc;
     }
+  }
+  __syncthreads();
+  if (tid < nt) {
+    const int t = tid;
+    const double s = ((part[t][0] + part[t][1]) + part[t][2]) + part[t][3];
+    logits[(int64_t)(t0 + t) * sl + e] = rstd ? (float)s * rstd[t0 + t] : (float)s;
   }
 }
 
@@ -347,13 +371,12 @@ int launch_logits(const void* y, int64_t stride_y, const void* wgt, int64_t stri
     if (stride_we < H || (stride_we % vec) || H > HMAX) return GLM52_EINVAL;
     *ks_out = 1;
     if (T == 0) return GLM52_OK;
-    dim3 grid((E + 3) / 4, (T + RT - 1) / RT);
-    const size_t lds = (size_t)(T < RT ? T : RT) * H * sizeof(uint16_t);  // <= 64 KB
+    dim3 grid(E, (T + RT - 1) / RT);
     auto* yy = static_cast<const uint16_t*>(y);
     if (wg_is_f32)
-      router_rows_kernel<true><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
+      router_rows_kernel<true><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
     else
-      router_rows_kernel<false><<<grid, 256, lds, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
+      router_rows_kernel<false><<<grid, 256, 0, stream>>>(yy, stride_y, wgt, stride_we, logits, stride_l, T, H, E, rstd);
     GLM52_RETURN_LAUNCH();
   }
   if (stride_we != 1 || stride_wk < E || (stride_wk % vec)) return GLM52_EINVAL;
