@@ -35,6 +35,8 @@ def _launch(x, res, w, h1, out, cfg, do_add: bool, do_norm: bool):
     if do_norm:
         _check("w", w)
         _check("out", out)
+    if T == 0:
+        return  # an empty batch: nothing to launch
     mode = cfg.get("WAVE_PER_ROW")
     mode = -1 if mode is None else int(bool(mode))
     _lib.call(

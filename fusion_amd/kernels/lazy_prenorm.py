@@ -68,6 +68,8 @@ def launch_router(a, b, c, cfg, fuse_norm: bool, eps: float = 1e-5, sq_mode: int
                   rstd=None):
     """`a`: [M,K] bf16.  `b`: [K,N] bf16.  `c`: [M,N] fp32."""
     M = a.shape[0]
+    if M == 0:
+        return  # an empty batch: nothing to launch
     if (fuse_norm or rstd is not None) and M <= 4 and b.stride(0) == 1:
         _rows_router(a, b, c, rstd, eps)
         return
@@ -109,6 +111,8 @@ def launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_pad
     """`a`: [T,K] bf16.  `b`: [E,N,K] bf16.  `c`: [T*top_k, N] bf16 (gate and up, unfused)."""
     T = a.shape[0]
     N = c.shape[1]
+    if T == 0:
+        return
     scale = None
     if fuse_norm or rstd is not None:
         # the per-slot scale rstd[f / top_k]; from the given rstd or computed here

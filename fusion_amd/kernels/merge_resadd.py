@@ -24,6 +24,8 @@ def _launch(y, wt, res, m, out, cfg, do_merge: bool, do_resadd: bool):
     else:
         T, N = m.shape
         syt = syk = 0
+    if T == 0:
+        return
     _lib.call(
         "glm52_merge_resadd",
         _lib.ptr(y) if do_merge else None, syt, syk,

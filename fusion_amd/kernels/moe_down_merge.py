@@ -57,6 +57,8 @@ def launch_down(a, w2, c, topk_weights_flat, sorted_token_ids, expert_ids,
                          f"c {tuple(c.shape)} (the merged [T, H] output), top_k={top_k}")
     bm = int(cfg["BLOCK_M"])
     cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    if num_valid_tokens == 0:
+        return
     _lib.call(
         "glm52_moe_down_merge", _lib.ptr(a), a.stride(0), _lib.ptr(w2), w2.stride(0),
         w2.stride(1), _lib.ptr(wp), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights_flat),
@@ -121,6 +123,8 @@ def launch_moe_sum(c3, out, residual, topk, cfg, add_residual: bool):
         c3 = c3.view(T, topk, Hd)
     if c3.stride(2) != 1 or out.stride(1) != 1:
         raise ValueError("moe_sum operands must be contiguous along H")
+    if T == 0:
+        return
     _lib.call(
         "glm52_moe_sum", _lib.ptr(c3), c3.stride(0), c3.stride(1), _lib.ptr(out), out.stride(0),
         _lib.ptr(residual) if add_residual else None,
@@ -132,6 +136,8 @@ def launch_moe_sum(c3, out, residual, topk, cfg, add_residual: bool):
 def launch_resadd(x, r, o, cfg):
     _lib.require_gpu(x, r, o)
     M, Nd = x.shape
+    if M == 0:
+        return
     _lib.call("glm52_resadd", _lib.ptr(x), x.stride(0), _lib.ptr(r), r.stride(0), _lib.ptr(o),
               o.stride(0), M, Nd, _lib.stream())
 

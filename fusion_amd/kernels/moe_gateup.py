@@ -59,6 +59,8 @@ def moe_gemm(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
     K = a.shape[1]
     if w.shape[2] != K:
         raise ValueError(f"K mismatch: A has {K}, W has {w.shape[2]}")
+    if num_valid_tokens == 0:
+        return  # no routed row: nothing to compute
     variant = VARIANTS[cfg.get("variant")]
     _lib.call(
         "glm52_moe_gemm", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w), w.stride(0),
@@ -99,6 +101,8 @@ def moe_gemm_packed(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids, e
         raise ValueError("topk weights must be a contiguous fp32 tensor")
     bm = int(cfg["BLOCK_M"])
     cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    if num_valid_tokens == 0:
+        return
     _lib.call(
         "glm52_moe_gemm_packed", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w_packed),
         _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights), _lib.ptr(sorted_token_ids),
@@ -129,6 +133,8 @@ def moe_gemm_shared(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_i
         raise ValueError("the fused shared-expert launch streams weights: BLOCK_M must be 16")
     cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
     K = a.shape[1]
+    if num_valid_tokens == 0 and a_shared.shape[0] == 0:
+        return
     _lib.call(
         "glm52_moe_gemm_shared", _lib.ptr(a), a.stride(0), int(a_row_div), _lib.ptr(w), w.stride(0),
         w.stride(1), int(gate_up_offset), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights),
@@ -173,5 +179,7 @@ def launch_silu_and_mul(x, y, cfg):
     M, two_i = x.shape
     if x.stride(1) != 1 or y.stride(1) != 1:
         raise ValueError("silu_and_mul operands must be row-contiguous")
+    if M == 0:
+        return
     _lib.call("glm52_silu_and_mul", _lib.ptr(x), x.stride(0), _lib.ptr(y), y.stride(0), M,
               two_i // 2, _lib.stream())

@@ -63,6 +63,8 @@ def router_gemm(x2, wgt, logits, cfg):
     """logits[T, E] fp32 = x2 . wgt; `cfg["workspace"]` may hold the split-K scratch."""
     _check_router_operands(x2, wgt, logits)
     T, H = x2.shape
+    if T == 0:
+        return  # an empty batch: nothing to launch
     E = wgt.shape[1]
     ws, need = _workspace(T, H, E, x2.device, cfg, wgt)
     _lib.call(
@@ -80,6 +82,8 @@ def router(x2, wgt, logits, topw, topi, cfg):
     if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
         raise ValueError("correction_bias must be a contiguous fp32 tensor")
     T, H = x2.shape
+    if T == 0:
+        return
     E = wgt.shape[1]
     ws, need = _workspace(T, H, E, x2.device, cfg, wgt)
     _lib.call(
@@ -99,6 +103,8 @@ def topk_only(logits, topw, topi, cfg):
         if bias.dtype != torch.float32 or not bias.is_contiguous():
             raise ValueError("correction_bias must be a contiguous fp32 tensor")
     T, E = logits.shape
+    if T == 0:
+        return
     k = topi.shape[1]
     _lib.call(
         "glm52_router_topk", _lib.ptr(logits), logits.stride(0), _lib.ptr(bias), _lib.ptr(topw),

@@ -93,6 +93,8 @@ def gemm_launch(a, b, c, r, cfg, fuse_resadd: bool, atomic_out: bool):
     if res is not None and (res.dtype != torch.bfloat16 or tuple(res.shape) != (M, N)
                             or res.stride(1) != 1):
         raise ValueError("r must be a [M, N] bf16 tensor with N contiguous")
+    if M == 0:
+        return  # an empty batch: nothing to launch
     decode = M <= 16 and b.stride(1) == 1
     splits = 1
     if not decode and a.stride(0) == K:
@@ -113,6 +115,8 @@ def epilogue_launch(c, r, o, cfg, has_res: bool):
     if c.dtype not in (torch.bfloat16, torch.float32) or o.dtype != torch.bfloat16:
         raise ValueError("c must be bf16 or fp32 and o bf16")
     M, N = o.shape
+    if M == 0:
+        return
     cv, ov = c.view(-1, N) if c.dim() != 2 else c, o
     _lib.call("glm52_cast_add", _lib.ptr(cv), int(c.dtype == torch.float32), cv.stride(0),
               _lib.ptr(rr), rr.stride(0) if rr is not None else 0, _lib.ptr(ov), ov.stride(0),
