@@ -16,8 +16,9 @@
 //
 // Mapping: one row of N bf16 is owned by TPR threads (TPR = 64: a wave per row, no
 // barrier; TPR = 256: a workgroup per row, for small T where latency matters).  Each
-// thread owns 8-element chunks c = tid_in_row + j * TPR, reads them with 128-bit loads,
-// keeps h in registers between the reduction and the normalisation, and writes with
+// thread owns 8-element chunks c = tid_in_row + j * TPR, issues all of its 128-bit loads
+// of x and r before its first store, keeps h (packed bf16) in registers between the
+// reduction and the normalisation, and writes with
 // 128-bit stores, so every byte of x, r, h and y crosses HBM exactly once.
 #include "common.h"
 
@@ -38,33 +39,36 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
   const bool row_ok = row < T;
   const int nchunk = N >> 3;
 
-  float hv[MAXC][8];
+  // every load of x and r is issued before the first store; h stays packed (it is bf16)
+  uint4 hb[MAXC], rv[MAXC];
+#pragma unroll
+  for (int j = 0; j < MAXC; ++j) {
+    const int c = t_in_row + j * TPR;
+    hb[j] = make_uint4(0, 0, 0, 0);
+    rv[j] = make_uint4(0, 0, 0, 0);
+    if (row_ok && c < nchunk) {
+      hb[j] = *reinterpret_cast<const uint4*>(x + row * sx + (int64_t)c * 8);
+      if (DO_ADD) rv[j] = *reinterpret_cast<const uint4*>(res + row * sr + (int64_t)c * 8);
+    }
+  }
   double ss = 0.0;
 #pragma unroll
   for (int j = 0; j < MAXC; ++j) {
     const int c = t_in_row + j * TPR;
     if (row_ok && c < nchunk) {
-      uint4 xv = *reinterpret_cast<const uint4*>(x + row * sx + (int64_t)c * 8);
       float xf[8];
-      unpack8(xv, xf);
+      unpack8(hb[j], xf);
       if (DO_ADD) {
-        uint4 rv = *reinterpret_cast<const uint4*>(res + row * sr + (int64_t)c * 8);
         float rf[8];
-        unpack8(rv, rf);
+        unpack8(rv[j], rf);
 #pragma unroll
         for (int q = 0; q < 8; ++q) xf[q] = xf[q] + rf[q];
-        uint4 hb = pack8(xf);
-        *reinterpret_cast<uint4*>(h1 + row * sh + (int64_t)c * 8) = hb;
-        unpack8(hb, xf);  // the norm consumes the bf16-rounded h
+        hb[j] = pack8(xf);
+        *reinterpret_cast<uint4*>(h1 + row * sh + (int64_t)c * 8) = hb[j];
+        unpack8(hb[j], xf);  // the norm consumes the bf16-rounded h
       }
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        hv[j][q] = xf[q];
-        ss += (double)(xf[q] * xf[q]);  // exact square, fp64 sum
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 8; ++q) hv[j][q] = 0.f;
+      for (int q = 0; q < 8; ++q) ss += (double)(xf[q] * xf[q]);  // exact square, fp64 sum
     }
   }
   if (!DO_NORM) return;
@@ -90,10 +94,11 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(
     const int c = t_in_row + j * TPR;
     if (c < nchunk) {
       uint4 wv = *reinterpret_cast<const uint4*>(w + (int64_t)c * 8);
-      float wf[8], yf[8];
+      float wf[8], hf[8], yf[8];
       unpack8(wv, wf);
+      unpack8(hb[j], hf);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) yf[q] = bf16_to_f32(f32_to_bf16(hv[j][q] * rstd)) * wf[q];
+      for (int q = 0; q < 8; ++q) yf[q] = bf16_to_f32(f32_to_bf16(hf[q] * rstd)) * wf[q];
       *reinterpret_cast<uint4*>(out + row * so + (int64_t)c * 8) = pack8(yf);
     }
   }
@@ -138,6 +143,9 @@ extern "C" int glm52_add_rmsnorm(const void* x, const void* res, const void* w, 
   auto* oo = static_cast<uint16_t*>(out);
   // rows_per_wave_mode: 1 -> a wave per row; 0 -> a workgroup per row; -1 -> choose by T.
   bool wave_per_row = rows_per_wave_mode > 0 || (rows_per_wave_mode < 0 && T >= 512);
+  if (wave_per_row && N <= 6144)  // the block's H: 12 chunks a lane, no idle registers
+    return launch<64, 12>(xx, rr, ww, hh, oo, stride_x, stride_r, stride_h, stride_o, T, N, eps,
+                          do_add, do_norm, stream);
   if (wave_per_row)
     return launch<64, 16>(xx, rr, ww, hh, oo, stride_x, stride_r, stride_h, stride_o, T, N, eps,
                           do_add, do_norm, stream);
