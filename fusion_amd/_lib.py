@@ -30,6 +30,7 @@ SIGNATURES: dict[str, list] = {
                                 _P, _P],
     "glm52_router_topk": [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _F, _I, _P],
     "glm52_moe_align": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
+    "glm52_moe_align_ws": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _L, _P],
     "glm52_decode_front": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L,
                            _I, _I, _I, _I, _F, _F, _I, _I, _I, _P, _P, _P, _P, _P],
     "glm52_decode_norm_logits": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I,
@@ -68,6 +69,7 @@ SIGNATURES: dict[str, list] = {
 # name -> (argument types, return type) for entry points that do not return a status
 QUERIES: dict[str, tuple[list, type]] = {
     "glm52_router_workspace_bytes": ([_I, _I, _I], c_int64),
+    "glm52_moe_align_workspace_bytes": ([_I, _I], c_int64),
     "glm52_packed_w512_bytes": ([_I, _I, _I, _I], c_int64),
     "glm52_oproj_workspace_bytes": ([_I, _I, _I], c_int64),
     "glm52_oproj_packed_bytes": ([_I, _I], c_int64),

@@ -40,7 +40,8 @@ import torch
 from . import config as C
 from . import _lib
 from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
-                       moe_align_block_size_into, route_gateup_shared_into, topk_align_into)
+                       align_workspace, moe_align_block_size_into, route_gateup_shared_into,
+                       topk_align_into)
 from .kernels import add_rmsnorm as KN
 from .kernels import moe_down_merge as KD
 from .kernels import norm_router as KR
@@ -112,6 +113,7 @@ class MoEBlock:
         self.sti = torch.empty(cap, dtype=torch.int32, device=dev)
         self.eids = torch.empty(cap // self.bm, dtype=torch.int32, device=dev)
         self.ntp = torch.empty(1, dtype=torch.int32, device=dev)
+        self.align_ws = align_workspace(R, E, dev)
         self.act = torch.empty(R, I, dtype=BF16, device=dev)
         self.ybuf = torch.empty(R, H, dtype=BF16, device=dev)
         self.act_s = torch.empty(T, I, dtype=BF16, device=dev)
@@ -162,7 +164,8 @@ class MoEBlock:
                             self.sti, self.eids, self.ntp)
         else:
             KR.router(self.y, self.wgt, self.logits, self.topw, self.topi, self.cfg_topk)
-            moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp)
+            moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp,
+                                      self.align_ws)
 
     def w13_step(self):
         """Steps 5 and 6 (at T <= 4 also 3 and 4): one launch when the shared expert runs

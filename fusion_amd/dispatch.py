@@ -24,19 +24,35 @@ def capacity(numel: int, block_m: int, num_experts: int) -> int:
     return ((need + block_m - 1) // block_m) * block_m
 
 
+def align_workspace(numel: int, num_experts: int, device) -> torch.Tensor | None:
+    """The chunk histograms of the multi-workgroup layout (None below 16384 ids, where one
+    workgroup builds it as fast)."""
+    n = _lib.query("glm52_moe_align_workspace_bytes", int(numel), int(num_experts))
+    return torch.empty(n // 4, dtype=torch.int32, device=device) if n else None
+
+
 def moe_align_block_size_into(topk_ids, block_m, num_experts, sorted_token_ids, expert_ids,
-                              num_tokens_post_padded):
-    """Destination-passing form (the caller owns the three buffers)."""
+                              num_tokens_post_padded, workspace="auto"):
+    """Destination-passing form (the caller owns the three buffers).  `workspace`: an int32
+    buffer from `align_workspace`, "auto" (allocated here when the input is large), or
+    None (the single-workgroup build, same result)."""
     _lib.require_gpu(topk_ids, sorted_token_ids, expert_ids, num_tokens_post_padded)
     if topk_ids.dtype != torch.int32 or not topk_ids.is_contiguous():
         raise ValueError("topk_ids must be a contiguous int32 tensor")
     cap = sorted_token_ids.numel()
     if expert_ids.numel() * block_m != cap:
         raise ValueError("expert_ids must hold capacity / block_m entries")
+    if isinstance(workspace, str):
+        workspace = align_workspace(topk_ids.numel(), num_experts, topk_ids.device)
+    if workspace is not None:
+        _lib.require_gpu(workspace)
+        if workspace.dtype != torch.int32 or not workspace.is_contiguous():
+            raise ValueError("the workspace is a contiguous int32 tensor")
     _lib.call(
-        "glm52_moe_align", _lib.ptr(topk_ids), topk_ids.numel(), int(block_m), int(num_experts),
-        cap, _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids),
-        _lib.ptr(num_tokens_post_padded), _lib.stream(),
+        "glm52_moe_align_ws", _lib.ptr(topk_ids), topk_ids.numel(), int(block_m),
+        int(num_experts), cap, _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids),
+        _lib.ptr(num_tokens_post_padded), _lib.ptr(workspace),
+        0 if workspace is None else workspace.numel() * 4, _lib.stream(),
     )
 
 

@@ -72,6 +72,20 @@ int glm52_moe_align(const int32_t* topk_ids, int numel, int block_m, int num_exp
                     int capacity, int32_t* sorted_token_ids, int32_t* expert_ids,
                     int32_t* num_tokens_post_padded, hipStream_t stream);
 
+/* The same layout for large inputs, by one workgroup per chunk of 2048 ids in two
+ * launches (chunk histograms, then prefix and stable scatter), with a caller-owned
+ * workspace of ceil(numel / 2048) * num_experts int32 histograms.  Same outputs, bit for
+ * bit, as glm52_moe_align, which it calls when the workspace is null or too small (or
+ * numel <= 2048).  glm52_moe_align_workspace_bytes(numel, num_experts) gives that size
+ * where the chunked build is the faster one (numel >= 16384), else 0.  No counterpart interface in
+ * the reference: a faster route to reference.moe_align_block_size
+ * (glm52/reference.py:85-128) for prefill sizes. */
+int64_t glm52_moe_align_workspace_bytes(int numel, int num_experts);
+int glm52_moe_align_ws(const int32_t* topk_ids, int numel, int block_m, int num_experts,
+                       int capacity, int32_t* sorted_token_ids, int32_t* expert_ids,
+                       int32_t* num_tokens_post_padded, void* workspace,
+                       int64_t workspace_bytes, hipStream_t stream);
+
 /* glm52_router_topk followed by glm52_moe_align in one single-workgroup launch, for
  * decode (T * topk <= 256).  Replaces the topk_only + moe_align_block_size pair
  * (glm52/kernels/norm_router.py:352-354, glm52/reference.py:85-128). */

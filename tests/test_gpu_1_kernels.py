@@ -12,8 +12,10 @@ import pytest
 import torch
 
 from fusion_amd import _lib
-from fusion_amd.dispatch import (capacity, decode_front_into, decode_norm_logits_into,
-                                 moe_align_block_size, route_gateup_shared_into, topk_align_into)
+from fusion_amd.dispatch import (align_workspace, capacity, decode_front_into,
+                                 decode_norm_logits_into, moe_align_block_size,
+                                 moe_align_block_size_into, route_gateup_shared_into,
+                                 topk_align_into)
 from fusion_amd.kernels import add_rmsnorm as KN
 from fusion_amd.kernels import merge_resadd as KM
 from fusion_amd.kernels import moe_down_merge as KD
@@ -365,6 +367,40 @@ def test_moe_align_skewed_routing(gpu):
         assert int(ntp.item()) == n
         assert np.array_equal(sti.cpu().numpy()[:n], rs)
         assert np.array_equal(eids.cpu().numpy()[: n // bm], re_)
+
+
+@pytest.mark.parametrize("numel,E,bm", [(2049, 256, 16), (4096, 7, 64), (30000, 160, 32),
+                                         (65536 + 13, 256, 128)])
+def test_moe_align_chunked_matches_single(gpu, numel, E, bm):
+    """The multi-workgroup layout (two launches over chunks of 2048 ids) against the
+    single-workgroup one, bit for bit, on ragged sizes with ids outside [0, E) mixed in
+    (both skip them), and against the oracle on the valid ids alone."""
+    say(f"align chunked numel={numel} E={E} bm={bm}")
+    rng = np.random.default_rng(numel + E)
+    ids = rng.integers(-2, E + 2, size=numel).astype(np.int32)
+    t = torch.from_numpy(ids).to(gpu)
+    cap = capacity(numel, bm, E)
+    # a workspace of ceil(numel / 2048) * E histograms selects the chunked build at any size
+    ws = torch.empty(-(-numel // 2048) * E, dtype=torch.int32, device=gpu)
+    want = align_workspace(numel, E, gpu)
+    assert (want is None) == (numel < 16384)
+    assert want is None or want.numel() == ws.numel()
+    got = []
+    for w in (None, ws):
+        sti = torch.full((cap,), -7, dtype=torch.int32, device=gpu)
+        eids = torch.full((cap // bm,), -7, dtype=torch.int32, device=gpu)
+        ntp = torch.full((1,), -7, dtype=torch.int32, device=gpu)
+        moe_align_block_size_into(t, bm, E, sti, eids, ntp, w)
+        got.append((sti.cpu(), eids.cpu(), ntp.cpu()))
+    for a, b in zip(*got):
+        assert torch.equal(a, b)
+    valid = np.where((ids >= 0) & (ids < E), ids, E)  # an extra expert E collects the rest
+    rs, re_, rn = O.moe_align_block_size(valid, bm, E + 1)
+    n = int(got[1][2][0])
+    keep = re_ < E  # drop the extra expert's blocks, which come last
+    assert n == int(keep.sum()) * bm
+    assert np.array_equal(got[1][0].numpy()[:n], rs[:n])
+    assert np.array_equal(got[1][1].numpy()[: n // bm], re_[keep])
 
 
 # ------------------------------------------------------------------ grouped GEMMs

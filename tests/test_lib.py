@@ -33,6 +33,17 @@ def test_router_workspace_query():
     assert KR.workspace_bytes(256) == 32 * 256 * 256 * 8  # 8 token blocks x 32 K slices
 
 
+def test_align_workspace_query():
+    q = lambda n, e: _lib.query("glm52_moe_align_workspace_bytes", n, e)  # noqa: E731
+    # one int32 histogram of E experts per chunk of 2048 ids, from 16384 ids up
+    assert q(65536, 256) == 32 * 256 * 4
+    assert q(16384, 256) == 8 * 256 * 4
+    assert q(16385, 160) == 9 * 160 * 4
+    assert q(16383, 256) == 0 and q(2048, 256) == 0
+    assert q(65536, 257) == 0 and q(65536, 0) == 0
+    assert q(1 << 21, 256) == 0  # past 512 chunks: the single-workgroup build
+
+
 def test_library_exports_every_declared_symbol():
     handle = _lib.lib()
     for name in declared_symbols():
