@@ -108,3 +108,13 @@ def test_default_block_m_regimes():
     assert block.default_block_m(8192) == 128
     assert [block.default_shared_block_m(T) for T in (1, 32, 256, 2048, 8192)] == [16, 64, 64,
                                                                                     128, 128]
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    """No CPU fallback: with the library absent every entry point raises."""
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libglm52_hip.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.call("glm52_moe_align", None, 0, 16, 256, 16, None, None, None, None)
+    with pytest.raises(RuntimeError, match="not built"):
+        _lib.query("glm52_moe_align_workspace_bytes", 65536, 256)
