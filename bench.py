@@ -1,12 +1,13 @@
 """Benchmark of the GLM-5.2 MoE FFN block on one MI355X.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 25] [--tokens 1,256,8192]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 25] [--tokens 1,256,2048,8192]
 
 A step is one pass of the whole block (ResAdd+RMSNorm -> router -> top-8 -> dispatch ->
 routed w13+SwiGLU / shared w13+SwiGLU -> routed w2 / shared w2 -> merge+ResAdd) over one
 batch of T synthetic tokens, with the real 256-expert weight set (19.3 GB) resident.
-The headline `value` is microseconds per block at T = 1 (configuration 1); T = 256 and
-8192 are reported under `per_T`.  Timing follows the reference's `bench_chain`
+The headline `value` is microseconds per block at T = 1 (configuration 1); T = 256, 2048
+and 8192 (configurations 2-4, the last with the skewed router bias, whose expert loads
+are reported with it) are under `per_T`.  Timing follows the reference's `bench_chain`
 (`glm52/common.py:73-122`): one cache flush (1 GiB, larger than the 256 MB Infinity
 Cache) before every step, never inside it, HIP events around the step, eager launches;
 decode sizes also report the replay of a captured HIP graph (`graph_us`).  The dominant kernel -- the block's w13 + SwiGLU
@@ -15,7 +16,8 @@ timed alone with events on its stream, for the `roofline` object; its HBM traffi
 from two `rocprofv3 --pmc` runs of a child process (`--pmc-child`), scaled by a plain
 copy of known size.  The CPU baseline is the oracle's restatement of
 `glm52/reference.py`'s path (fp32 router, per-expert bf16 `moe_mlp`, fp32 shared expert)
-on this host's cores at T = 1.
+on all of this host's cores at every T of `--tokens` (median of 5 blocks at T <= 256, 3 at
+2048, 1 at 8192), with the CPU model recorded.
 """
 
 from __future__ import annotations
@@ -41,7 +43,7 @@ def parse():
     # 25 untimed steps, as the reference's bench_chain: the first ~25 blocks of a fresh
     # process run slower (measured at T = 1: 128-130 us, then 121-122 us)
     ap.add_argument("--warmup", type=int, default=25)
-    ap.add_argument("--tokens", default="1,256,8192",
+    ap.add_argument("--tokens", default="1,256,2048,8192",
                     help="token counts; the first is the headline (configuration 1 is T=1)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -144,7 +146,9 @@ def main() -> int:
                        W.w13s, W.w2s)
         blk(x, r)
         torch.cuda.synchronize()
-        n_e = int(torch.unique(blk.topi).numel())
+        loads = torch.bincount(blk.topi.reshape(-1).long(), minlength=blk.E).cpu()
+        n_e = int((loads > 0).sum())
+        top20 = float(loads.sort(descending=True).values[: blk.E // 5].sum() / loads.sum())
         # the headline times eager launches, as the reference's bench_chain does; decode
         # sizes also time a captured HIP graph of the same chain (reported, not headline:
         # on this ROCm its replay adds launch gaps between the nodes)
@@ -175,6 +179,11 @@ def main() -> int:
             "w13_launch": w13_kernel_name(blk),
             "block_m": blk.bm,
             "bias": bias,
+            # expert loads (slots per expert): the share the busiest 20 % of experts take,
+            # and the largest and smallest load among the experts hit
+            "top20_share": round(top20, 4),
+            "max_load": int(loads.max()),
+            "min_load": int(loads[loads > 0].min()),
         }
         if not args.no_oproj:
             rec["down_merge"] = down_merge_bench(blk, W, T, n_e, timed, args.steps, args.warmup)
@@ -194,7 +203,7 @@ def main() -> int:
             "algorithmic_bytes": int(kc.bytes), "avg_us": round(k_us, 2)}
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(W, tokens[0], args.cpu_seconds)
+        cpu = cpu_baseline(W, tokens, args.cpu_seconds)
     del W, flush_buf
     torch.cuda.empty_cache()
     if not args.no_traffic:
@@ -466,42 +475,102 @@ def calibrate(dev) -> list:
     return out
 
 
-def cpu_baseline(W, T: int, seconds: float) -> dict:
-    """The oracle's restatement of the reference path at T tokens on the host cores."""
+def cpu_model() -> str:
+    """The host CPU's model name (as `lscpu` prints it), from /proc/cpuinfo."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+# repetitions per T (median reported), the plan of the reference's CPU baseline; T = 1
+# runs for `--cpu-seconds` instead
+CPU_REPS = {256: 5, 2048: 3, 8192: 1}
+CPU_BUDGET_S = 150.0  # whole CPU leg; a T whose one block is predicted past it is skipped
+
+
+def cpu_baseline(W, tokens: list, seconds: float) -> dict:
+    """The oracle's restatement of the reference path on all of the host's cores, at every
+    T of `tokens`: add_rmsnorm, the fp32 router with the correction bias, the per-expert
+    bf16 `moe_mlp` and the fp32 shared expert, composed as `glm52/bench/bench_layer.py:365-374`.
+    `value` is the first T (configuration 1); the others are under `per_T`."""
     import torch
 
     from fusion_amd.problem import front_end
     from oracle import glm52_oracle as O
 
-    ncores = min(16, os.cpu_count() or 1)
+    ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
-    fe = front_end(T)
-    y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
-    _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
-    experts = sorted(set(ti.view(-1).tolist()))
-    w13 = {e: W.w13[e].cpu() for e in experts}
-    w2 = {e: W.w2[e].cpu() for e in experts}
     w13s, w2s = W.w13s.cpu(), W.w2s.cpu()
+    full = None  # the whole expert stack on the host, copied once for T > 1
+    per_T = {}
+    t_leg = time.perf_counter()
+    last = None  # (T, seconds per block) of the previous T, to predict the next
+    for T in tokens:
+        fe = front_end(T, bias="zipf" if T == 8192 else "normal")
+        if T == 1:
+            y, _ = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+            _, _, ti = O.router_reference(y, fe.gate, fe.bias)
+            experts = sorted(set(ti.view(-1).tolist()))
+            w13 = {e: W.w13[e].cpu() for e in experts}
+            w2 = {e: W.w2[e].cpu() for e in experts}
 
-    def block():
-        y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
-        _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
-        routed = O.moe_mlp_rows(y, w13, w2, tw, ti, list(range(T))).to(torch.bfloat16).float()
-        s = O.shared_expert(y, w13s, w2s)
-        return (routed + h.float() + s).to(torch.bfloat16)
+            def block():
+                y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+                _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
+                routed = O.moe_mlp_rows(y, w13, w2, tw, ti, [0]).to(torch.bfloat16).float()
+                return (routed + h.float() + O.shared_expert(y, w13s, w2s)).to(torch.bfloat16)
+        else:
+            if full is None:
+                full = (W.w13.cpu(), W.w2.cpu())
 
-    block()
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        block()
-        times.append(time.perf_counter() - t0)
-    return {"value": round(statistics.median(times) * 1e6, 1), "unit": "us", "cores": ncores,
-            "kind": "port",
-            "sample": f"{len(times)} full blocks at T={T} (configuration 1) over ~{seconds:.0f}s; "
-                      f"torch-CPU fp32 router + per-expert bf16 moe_mlp + fp32 shared expert, "
-                      f"median"}
+            def block():
+                y, h = O.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+                _, tw, ti = O.router_reference(y, fe.gate, fe.bias)
+                routed = O.moe_mlp(y, full[0], full[1], tw, ti).float()
+                return (routed + h.float() + O.shared_expert(y, w13s, w2s)).to(torch.bfloat16)
+        left = CPU_BUDGET_S - (time.perf_counter() - t_leg)
+        if last is not None:
+            predicted = last[1] * T / last[0]
+            if predicted > left:
+                per_T[str(T)] = {"us": None, "reps": 0,
+                                 "note": f"skipped: one block predicted {predicted:.0f}s, "
+                                         f"{max(left, 0):.0f}s of the CPU leg left"}
+                log(f"cpu baseline T={T}: {per_T[str(T)]['note']}")
+                continue
+        times = []
+        if T == 1:
+            block()  # warm
+            t_end = time.perf_counter() + seconds
+            while time.perf_counter() < t_end or len(times) < 3:
+                t0 = time.perf_counter()
+                block()
+                times.append(time.perf_counter() - t0)
+        else:
+            for _ in range(CPU_REPS.get(T, 1)):
+                t0 = time.perf_counter()
+                block()
+                times.append(time.perf_counter() - t0)
+                if time.perf_counter() - t_leg > CPU_BUDGET_S:
+                    break
+        med = statistics.median(times)
+        last = (T, med)
+        per_T[str(T)] = {"us": round(med * 1e6, 1), "reps": len(times)}
+        log(f"cpu baseline T={T}: {per_T[str(T)]}")
+    del full
+    T0 = tokens[0]
+    return {"value": per_T[str(T0)]["us"], "unit": "us", "cores": ncores, "kind": "port",
+            "cpu_model": cpu_model(),
+            "sample": f"full blocks at T={T0} (configuration 1), median of "
+                      f"{per_T[str(T0)]['reps']} over ~{seconds:.0f}s; torch-CPU fp32 router + "
+                      f"per-expert bf16 moe_mlp + fp32 shared expert on {ncores} threads; "
+                      f"other T under per_T (median of 5 at T<=256, 3 at 2048, 1 at 8192)",
+            "per_T": per_T}
 
 
 if __name__ == "__main__":

@@ -133,6 +133,11 @@ class MoEBlock:
         # expert and h in one launch (no Y rows, no merge launch)
         self.token_major = (self.front_fused and variant is None) if token_major is None \
             else bool(token_major)
+        if self.token_major and not self.shared_fused:
+            # the token-major tail reads the shared expert's activations, which only the
+            # weight-streaming w13 launch (block size 16) writes before the tail
+            raise ValueError("token_major needs the weight-streaming layout (block size 16, "
+                             f"T <= 384); T={T} runs block size {self.bm}")
         self.gate_rows = wgt.t().contiguous() if self.decode else None  # [E, H]
         self.wgt_rows = self.gate_rows.t() if self.decode else None  # its [H, E] view
         need = KR.workspace_bytes(T, H, E)

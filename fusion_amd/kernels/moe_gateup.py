@@ -84,7 +84,24 @@ def pack_w512(w, n_out: int, gate_up_offset: int, gated: bool) -> torch.Tensor:
     out = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=w.device)
     _lib.call("glm52_pack_w512", _lib.ptr(w), w.stride(0), w.stride(1), E, int(n_out), K,
               int(gate_up_offset), int(gated), _lib.ptr(out), _lib.stream())
+    out.glm52_pack = (E, int(n_out), K, bool(gated))  # checked by moe_gemm_packed
     return out
+
+
+def check_packed(w_packed, n_out: int, K: int, gated: bool) -> None:
+    """Reject a packed buffer made for another shape: one from `pack_w512` must carry the
+    same (n_out, K, gated); a bare buffer must hold a whole number of experts' packed W."""
+    tag = getattr(w_packed, "glm52_pack", None)
+    if tag is not None:
+        if tag[1:] != (int(n_out), int(K), bool(gated)):
+            raise ValueError(f"w_packed was packed for (n_out, K, gated) = {tag[1:]}, "
+                             f"not {(int(n_out), int(K), bool(gated))}")
+        return
+    per = _lib.query("glm52_packed_w512_bytes", 1, int(n_out), int(K), int(gated))
+    have = w_packed.numel() * 2
+    if per <= 0 or have == 0 or have % per:
+        raise ValueError(f"w_packed ({have} bytes) is not a whole number of experts packed "
+                         f"for n_out={n_out}, K={K}, gated={bool(gated)}")
 
 
 def moe_gemm_packed(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids, expert_ids,
@@ -99,6 +116,9 @@ def moe_gemm_packed(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids, e
     if topk_weights is not None and (topk_weights.dtype != torch.float32
                                      or not topk_weights.is_contiguous()):
         raise ValueError("topk weights must be a contiguous fp32 tensor")
+    if not w_packed.is_contiguous():
+        raise ValueError("w_packed must be contiguous")
+    check_packed(w_packed, n_out, a.shape[1], gated)
     bm = int(cfg["BLOCK_M"])
     cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
     if num_valid_tokens == 0:

@@ -15,7 +15,8 @@ A is [M, K] bf16, B is [K, N] bf16 with any strides (the reference passes the nn
 weight transposed and made contiguous).  Decode (M <= 16, B N-contiguous) streams B
 through a split-K kernel with a fixed-order reduction; every other case runs the MoE
 block's 512-row tile GEMM on a packed copy of B, made on first use and cached on the
-tensor's storage, shape, strides and version counter (an in-place update of B re-packs).
+tensor's address, shape, strides and version counter while that tensor lives (an in-place
+update of B re-packs; a new B at a freed B's address re-packs).
 When M gives too few 512-row tiles to fill the GPU (M up to a few hundred), the K range
 is cut into slices run as separate experts into fp32 partials, summed in slice order.
 Triton mapping keys in `cfg` (BLOCK_M/N/K, GROUP_M, SPLIT_K, num_warps, num_stages) are
@@ -25,15 +26,20 @@ chain builders, as in the reference.
 
 from __future__ import annotations
 
+import weakref
 from collections import OrderedDict
 
 import torch
 
 from .. import _lib
 
-_PACKED: "OrderedDict[tuple, torch.Tensor]" = OrderedDict()
+# key -> (weak reference to the B that was packed, packed copy)
+_PACKED: "OrderedDict[tuple, tuple]" = OrderedDict()
 _PACK_CACHE_SIZE = 4
+# (device, stream) -> workspace; outgrown ones are kept (a captured graph may still use
+# them), and each new one at least doubles, so few are ever kept
 _WORKSPACE: dict = {}
+_RETIRED: list = []
 
 
 def smem_bytes(cfg: dict) -> int:
@@ -48,22 +54,34 @@ def _workspace(dev, nbytes: int, cfg: dict) -> torch.Tensor:
         if ws.numel() * ws.element_size() < nbytes:
             raise ValueError(f"cfg workspace holds fewer than the {nbytes} bytes needed")
         return ws
-    key = (dev.type, dev.index)
+    key = (dev.type, dev.index, _lib.stream())
     ws = _WORKSPACE.get(key)
     if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=dev)
+        if ws is not None:
+            _RETIRED.append(ws)
+        grown = max(nbytes, 1 << 20, 2 * (ws.numel() if ws is not None else 0))
+        ws = torch.empty(grown, dtype=torch.uint8, device=dev)
         _WORKSPACE[key] = ws
     return ws
 
 
 def packed_weight(b: torch.Tensor, splits: int = 1) -> torch.Tensor:
     """The packed copy of B ([K, N] bf16, cut into `splits` K slices) the prefill mapping
-    reads, cached."""
+    reads, cached.
+
+    A hit needs the tensor that was packed to be alive (and to share B's storage): while
+    it lives its memory cannot be handed to another tensor, so an equal address, shape,
+    strides and version counter mean equal contents.  Once it is freed the entry is dead,
+    even if a new weight later lands at the same address with the same version."""
     key = (b.device.index, b.data_ptr(), tuple(b.shape), tuple(b.stride()), b._version, splits)
     hit = _PACKED.get(key)
     if hit is not None:
-        _PACKED.move_to_end(key)
-        return hit
+        src = hit[0]()
+        if src is not None and (src is b or src.untyped_storage().data_ptr()
+                                == b.untyped_storage().data_ptr()):
+            _PACKED.move_to_end(key)
+            return hit[1]
+        del _PACKED[key]
     K, N = b.shape
     nbytes = _lib.query("glm52_oproj_packed_bytes", K, N)
     if nbytes < 0:
@@ -71,7 +89,7 @@ def packed_weight(b: torch.Tensor, splits: int = 1) -> torch.Tensor:
     out = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=b.device)
     _lib.call("glm52_oproj_pack", _lib.ptr(b), b.stride(0), b.stride(1), K, N, int(splits),
               _lib.ptr(out), _lib.stream())
-    _PACKED[key] = out
+    _PACKED[key] = (weakref.ref(b), out)
     while len(_PACKED) > _PACK_CACHE_SIZE:
         _PACKED.popitem(last=False)
     return out

@@ -1,13 +1,16 @@
 """Write the golden vectors of the reference's own fp32/bf16 path (run once, on the CPU,
 in the build container that holds the reference checkout; the outputs are committed).
 
-    python tests/golden/make_golden.py [/path/to/reference]
+    python tests/golden/make_golden.py [/path/to/reference] [all|routing]
 
 It imports `glm52.reference` from the reference checkout only for the functions whose
 bit-level behaviour no closed form pins (torch's reduction order inside `rmsnorm`, the
 router's `F.linear` and `topk`, torch's `silu` rounding, the CPU bf16 `F.linear` inside
-`moe_mlp`, the fp32 product-sum of `expert_merge`).  The dispatch layout is integer work
-pinned by brute force and invariants, so it is not taken from here.
+`moe_mlp`, the fp32 product-sum of `expert_merge`), and for the routing of every
+benchmark token count: the reference's own chain `add_rmsnorm -> router ->
+moe_align_block_size` (`glm52/reference.py:28-33`, `:46-79`, `:85-128`) at T = 1, 4
+(Zipf bias), 16, 32, 256, 2048 and 8192 (Zipf bias), whose ids and layouts the device
+must reproduce bit for bit.
 
 Inputs are not stored: they are regenerated from seeds by `fusion_amd.problem` (and by
 the tiny-shape generator below); the SHA-256 of every input is stored so a drift of the
@@ -52,9 +55,13 @@ def tiny_inputs(seed: int = 99, T: int = 16, H: int = 256, I: int = 128, E: int 
     return dict(x=x, gate=gate, w13=w13, w2=w2, w13s=w13s, w2s=w2s, act_in=act_in, y3=y3, wt=wt)
 
 
-def main(ref_root: str) -> None:
+def main(ref_root: str, what: str = "all") -> None:
     sys.path.insert(0, ref_root)
     from glm52 import reference as R  # the reference's oracle, CPU only
+
+    if what == "routing":
+        routing_fixtures(R)
+        return
 
     # ---- configuration 0: T = 32 front end -------------------------------------------
     fe = front_end(32)
@@ -83,7 +90,61 @@ def main(ref_root: str) -> None:
         silu=u16(act), merged=u16(merged),
     )
     print("wrote", HERE / "config0_t32.npz", HERE / "tiny_moe.npz")
+    routing_fixtures(R)
+
+
+# the token counts and bias kinds of the block's GPU parity cases
+ROUTING_CASES = [(1, "normal"), (4, "zipf"), (16, "normal"), (32, "normal"), (256, "normal"),
+                 (2048, "normal"), (8192, "zipf")]
+BLOCK_MS = (16, 64, 128)
+
+
+def routing_path(T: int, bias: str) -> Path:
+    return HERE / f"routing_t{T}_{bias}.npz"
+
+
+def i32_sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(np.asarray(a, dtype=np.int32)).tobytes()).hexdigest()
+
+
+def routing_fixtures(R) -> None:
+    """The reference's routing at each case: ids, weights and the three layouts.
+
+    Stored per case: the input digests; the digests of the reference's h and y, and the
+    positions and values where its y differs from the order-independent statistic of the
+    oracle (`add_rmsnorm_exact`, the device rule) -- so the reference's y is pinned
+    entirely; ids (uint8, E = 256), fp32 weights; for block sizes 16, 64 and 128 the
+    digests of sorted_token_ids / expert_ids (int32, exact sizes) and the padded count,
+    plus the arrays themselves for T <= 256.
+    """
+    from oracle import glm52_oracle as O
+
+    for T, bias in ROUTING_CASES:
+        fe = front_end(T, bias=bias)
+        y, h = R.add_rmsnorm(fe.x, fe.r, fe.w_norm)
+        _, tw, ti = R.router(y, fe.gate, fe.bias)
+        y_ex, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+        yr, ye = u16(y).reshape(-1), u16(y_ex).reshape(-1)
+        diff = np.nonzero(yr != ye)[0]
+        rec = dict(
+            in_sha=np.array([sha(fe.x), sha(fe.r), sha(fe.w_norm), sha(fe.gate), sha(fe.bias)]),
+            h_sha=np.array(sha(h)), y_sha=np.array(sha(y)),
+            y_patch_pos=diff.astype(np.int64), y_patch_val=yr[diff],
+            topk_ids=ti.numpy().astype(np.uint8), topk_weights=tw.numpy(),
+        )
+        for bm in BLOCK_MS:
+            sti, eids, ntp = R.moe_align_block_size(ti, bm, 256)
+            rec[f"ntp_{bm}"] = np.array(int(ntp[0]))
+            rec[f"sti_sha_{bm}"] = np.array(i32_sha(sti.numpy()))
+            rec[f"eids_sha_{bm}"] = np.array(i32_sha(eids.numpy()))
+            if T <= 256:
+                rec[f"sti_{bm}"] = sti.numpy().astype(np.int32)
+                rec[f"eids_{bm}"] = eids.numpy().astype(np.int32)
+        np.savez_compressed(routing_path(T, bias), **rec)
+        print(f"wrote {routing_path(T, bias).name}: y differs from the exact statistic in "
+              f"{diff.size} elements", flush=True)
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference",
+         sys.argv[2] if len(sys.argv) > 2 else "all")

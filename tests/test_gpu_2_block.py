@@ -3,7 +3,9 @@ resident, at the token counts of the benchmark configurations.
 
 * front end (h, y, logits, ids, weights) and the dispatch layout: bit for bit against
   the CPU oracle's exact rule;
-* block output on sampled tokens, against references computed in fp32 with torch on the
+* routing ids and the dispatch layout: bit for bit against the reference's own chain
+  (fixtures written from `glm52/reference.py` on the CPU);
+* block output on every token row, against references computed in fp32 with torch on the
   GPU (floating-point references of the same op): within rtol 2e-2 / atol 2e-2 of the
   fp32 ground truth, and within the reference's own `rel_err <= 2e-2` gate
   (`glm52/common.py:186-200`) of its framework-faithful path
@@ -12,6 +14,9 @@ resident, at the token counts of the benchmark configurations.
 """
 
 from __future__ import annotations
+
+import hashlib
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -23,6 +28,8 @@ from fusion_amd.problem import expert_weights, front_end
 from oracle import glm52_oracle as O
 
 pytestmark = pytest.mark.gpu
+
+GOLD = Path(__file__).resolve().parent / "golden"
 
 BF16 = torch.bfloat16
 
@@ -45,8 +52,9 @@ def u16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
 
-def rows_reference(y, h, ids, tw, W, rows):
-    """Two references for token rows `rows`, computed in fp32 on the GPU.
+def block_references(y, h, ids, tw, W):
+    """Two references for every token row, computed in fp32 on the GPU, one expert at a
+    time (each expert's slots as one batch; fp32 GEMMs, no bf16 products involved).
 
     exact:    the fp32 ground truth -- fp32 GEMMs, fp32 SwiGLU, fp32 weighted sum and
               fp32 shared expert, one bf16 rounding at the end (`moe_mlp_exact_fp32`,
@@ -55,27 +63,41 @@ def rows_reference(y, h, ids, tw, W, rows):
               bf16 w2 linear, bf16 routed sum (`glm52/reference.py:134-156`), + h, + the
               shared expert of `glm52/bench/bench_layer.py:369-372`.
     """
-    exact, faithful = [], []
-    silu = torch.nn.functional.silu
+    silu = F.silu
+    T, H = y.shape
     I = W.w2.shape[2]
-    for t in rows:
-        yt = y[t].float()
-        acc_x = torch.zeros(y.shape[1], dtype=torch.float32, device=y.device)
-        acc_f = torch.zeros_like(acc_x)
-        for k in range(ids.shape[1]):
-            e, wk = int(ids[t, k]), float(tw[t, k])
-            hh = W.w13[e].float() @ yt
-            acc_x += wk * (W.w2[e].float() @ (silu(hh[:I]) * hh[I:]))
-            hb = hh.to(BF16).float()
-            a = (silu(hb[:I]) * hb[I:]).to(BF16).float()
-            acc_f += (W.w2[e].float() @ a).to(BF16).float() * wk
-        sh = W.w13s[0].float() @ yt
-        sy_x = W.w2s[0].float() @ (silu(sh[:I]) * sh[I:])
-        shb = sh.to(BF16).float()
-        sy_f = W.w2s[0].float() @ (silu(shb[:I]) * shb[I:]).to(BF16).float()
-        exact.append((acc_x + h[t].float() + sy_x).to(BF16))
-        faithful.append((acc_f.to(BF16).float() + h[t].float() + sy_f).to(BF16))
-    return torch.stack(exact), torch.stack(faithful)
+    yf = y.float()
+    acc_x = torch.zeros(T, H, dtype=torch.float32, device=y.device)
+    acc_f = torch.zeros_like(acc_x)
+    flat = ids.reshape(-1).to(y.device).long()
+    wflat = tw.reshape(-1).to(y.device).float()
+    order = torch.argsort(flat, stable=True)
+    counts = torch.bincount(flat, minlength=W.w13.shape[0]).tolist()
+    start = 0
+    for e, c in enumerate(counts):
+        if c == 0:
+            continue
+        sel = order[start:start + c]
+        start += c
+        tok, wk = sel // ids.shape[1], wflat[sel].unsqueeze(1)
+        hh = yf[tok] @ W.w13[e].float().t()
+        w2t = W.w2[e].float().t()
+        acc_x.index_add_(0, tok, wk * ((silu(hh[:, :I]) * hh[:, I:]) @ w2t))
+        hb = hh.to(BF16).float()
+        a = (silu(hb[:, :I]) * hb[:, I:]).to(BF16).float()
+        acc_f.index_add_(0, tok, (a @ w2t).to(BF16).float() * wk)
+    sh = yf @ W.w13s[0].float().t()
+    w2st = W.w2s[0].float().t()
+    sy_x = (silu(sh[:, :I]) * sh[:, I:]) @ w2st
+    shb = sh.to(BF16).float()
+    sy_f = (silu(shb[:, :I]) * shb[:, I:]).to(BF16).float() @ w2st
+    exact = (acc_x + h.float() + sy_x).to(BF16)
+    faithful = (acc_f.to(BF16).float() + h.float() + sy_f).to(BF16)
+    return exact, faithful
+
+
+def i32_sha(a) -> str:
+    return hashlib.sha256(np.ascontiguousarray(np.asarray(a, dtype=np.int32)).tobytes()).hexdigest()
 
 
 CONFIGS = [(1, "normal"), (4, "zipf"), (16, "normal"), (32, "normal"), (256, "normal"),
@@ -106,20 +128,27 @@ def test_block_parity(gpu, weights, T, bias):
     assert np.array_equal(blk.sti.cpu().numpy()[:n], rs)
     assert np.array_equal(blk.eids.cpu().numpy()[: n // blk.bm], re_)
 
-    # block output on sampled tokens vs the fp32 ground truth
-    g = torch.Generator().manual_seed(T)
-    rows = sorted(set([0, T - 1] + torch.randint(0, T, (6,), generator=g).tolist()))
-    exact, faithful = rows_reference(blk.y, blk.h, blk.topi.cpu(), blk.topw.cpu(), weights,
-                                     rows)
-    got = out[rows]
-    assert torch.isfinite(got.float()).all()
-    err_x = O.rel_err(got.cpu(), exact.cpu())
-    err_f = O.rel_err(got.cpu(), faithful.cpu())
-    say(f"  rel_err vs fp32 ground truth {err_x:.3e}, vs framework path {err_f:.3e}")
+    # routing and layout: bit for bit against the reference's own chain
+    # (`glm52/reference.py:28-128`, fixtures written on the CPU by tests/golden/make_golden.py)
+    g = np.load(GOLD / f"routing_t{T}_{bias}.npz")
+    assert np.array_equal(blk.topi.cpu().numpy(), g["topk_ids"].astype(np.int32))
+    assert n == int(g[f"ntp_{blk.bm}"])
+    assert i32_sha(blk.sti.cpu().numpy()[:n]) == str(g[f"sti_sha_{blk.bm}"])
+    assert i32_sha(blk.eids.cpu().numpy()[: n // blk.bm]) == str(g[f"eids_sha_{blk.bm}"])
+
+    # block output on every token row vs the fp32 ground truth
+    exact, faithful = block_references(blk.y, blk.h, blk.topi, blk.topw, weights)
+    assert torch.isfinite(out.float()).all()
+    err_x = O.rel_err(out.cpu(), exact.cpu())
+    err_f = O.rel_err(out.cpu(), faithful.cpu())
+    say(f"  all {T} rows: rel_err vs fp32 ground truth {err_x:.3e}, vs framework path {err_f:.3e}")
     # north-star tolerance against the fp32 ground truth
-    torch.testing.assert_close(got.float(), exact.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(out.float(), exact.float(), rtol=2e-2, atol=2e-2)
     # the reference's own gate against its framework path (`glm52/common.py:186-200`)
     assert err_f <= 2e-2
+    # per-token gate as well: no row is hidden by the max over the whole batch
+    row_err = (out.float() - faithful.float()).abs().amax(1) / faithful.float().abs().amax(1)
+    assert float(row_err.max()) <= 2e-2
 
     # determinism: a second launch gives the same bits
     out2 = blk(x, r)
@@ -127,7 +156,7 @@ def test_block_parity(gpu, weights, T, bias):
     assert torch.equal(out2, out)
 
 
-@pytest.mark.parametrize("T", [1, 256])
+@pytest.mark.parametrize("T", [1, 256, 2048])
 def test_block_graph_replay(gpu, weights, T):
     say(f"graph replay T={T}")
     fe = front_end(T)
@@ -144,3 +173,77 @@ def test_block_graph_replay(gpu, weights, T):
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"replay {i} differs from eager"
         _ = (x.float() * 2).sum().item()  # eager work between replays
+
+
+@pytest.fixture
+def glm52_names():
+    from fusion_amd import binding
+
+    bound = binding.install()
+    yield bound
+    binding.uninstall()
+
+
+@pytest.mark.parametrize("T,bias", [(32, "normal"), (2048, "normal")])
+def test_reference_chain_through_glm52_names(gpu, weights, glm52_names, T, bias):
+    """The reference's `H_f3_f10` launch sequence without o_proj
+    (`glm52/bench/bench_layer.py:417-480`: fused_add_rmsnorm, router_gemm, topk_only,
+    launch_gateup(fused), launch_down, launch_moe_sum(add_residual), and the shared
+    expert's launch_gateup + launch_silu_and_mul + launch_down + launch_resadd), written
+    against the reference's module names bound to this build, with the layout from
+    `glm52.reference.moe_align_block_size`.  Routing and layout must equal the reference's
+    own (fixtures) bit for bit, and the output must sit within the north-star tolerance of
+    the fp32 ground truth."""
+    from glm52 import reference as R
+    from glm52.kernels import add_rmsnorm as KN
+    from glm52.kernels import moe_down_merge as KD
+    from glm52.kernels import moe_gateup as KG
+    from glm52.kernels import norm_router as KR
+
+    say(f"reference chain through glm52.* names, T={T}")
+    E, H, I, TOPK = 256, 6144, 2048, 8
+    fe = front_end(T, bias=bias)
+    c, h_in = fe.x.to(gpu), fe.r.to(gpu)
+    w_norm, wg_t, bias_t = fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu)
+    rows = T * TOPK
+    z = lambda *s, dt=BF16: torch.empty(*s, dtype=dt, device=gpu)  # noqa: E731
+    h1, x2 = z(T, H), z(T, H)
+    logits, topw, topi = z(T, E, dt=torch.float32), z(T, TOPK, dt=torch.float32), \
+        z(T, TOPK, dt=torch.int32)
+    act, y3 = z(rows, I), torch.zeros(rows, H, dtype=BF16, device=gpu)
+    out = z(T, H)
+    s_inter, s_act, s_out = z(T, 2 * I), z(T, I), z(T, H)
+    ones = torch.ones(T, dtype=torch.float32, device=gpu)
+    bm = 16 if T <= 256 else 128
+    sbm = 16 if T <= 256 else 128
+
+    KN.fused_add_rmsnorm(c, h_in, w_norm, h1, x2, {})
+    rcfg = {"correction_bias": bias_t, "scale": 2.5}
+    KR.router_gemm(x2, wg_t, logits, rcfg)
+    KR.topk_only(logits, topw, topi, rcfg)
+    sti, eid, ntp = R.moe_align_block_size(topi, bm, E)
+    KG.launch_gateup(x2, weights.w13, act, sti, eid, ntp, rows, TOPK, I, {"BLOCK_M": bm}, True)
+    tw_flat = topw.flatten().contiguous()
+    KD.launch_down(act, weights.w2, y3, tw_flat, sti, eid, ntp, rows, TOPK, {"BLOCK_M": bm},
+                   False)
+    KD.launch_moe_sum(y3.view(T, TOPK, H), out, h1, TOPK, {}, True)
+    ssti, seid, sntp = R.moe_align_block_size(torch.zeros(T, 1, dtype=torch.int32, device=gpu),
+                                              sbm, 1)
+    KG.launch_gateup(x2, weights.w13s, s_inter, ssti, seid, sntp, T, 1, I, {"BLOCK_M": sbm},
+                     False)
+    KG.launch_silu_and_mul(s_inter, s_act, {})
+    KD.launch_down(s_act, weights.w2s, s_out, ones, ssti, seid, sntp, T, 1, {"BLOCK_M": sbm},
+                   False)
+    KD.launch_resadd(s_out, out, out, {})
+    torch.cuda.synchronize()
+
+    g = np.load(GOLD / f"routing_t{T}_{bias}.npz")
+    assert np.array_equal(topi.cpu().numpy(), g["topk_ids"].astype(np.int32))
+    n = int(ntp.item())
+    assert sti.numel() == n and eid.numel() == n // bm  # the reference's exact sizes
+    assert n == int(g[f"ntp_{bm}"])
+    assert i32_sha(sti.cpu().numpy()) == str(g[f"sti_sha_{bm}"])
+    assert i32_sha(eid.cpu().numpy()) == str(g[f"eids_sha_{bm}"])
+    exact, faithful = block_references(x2, h1, topi, topw, weights)
+    torch.testing.assert_close(out.float(), exact.float(), rtol=2e-2, atol=2e-2)
+    assert O.rel_err(out.cpu(), faithful.cpu()) <= 2e-2

@@ -108,3 +108,27 @@ def test_oproj_rejects_wrong_output_dtype(gpu):
     a, _, b, r = _problem(1, 1024, gpu)
     with pytest.raises(ValueError, match="must be"):
         KO.gemm_launch(a, b, torch.empty(1, N_OUT, dtype=BF16, device=gpu), r, {}, True, True)
+
+
+def test_oproj_pack_cache_misses_a_new_weight_at_a_freed_address(gpu):
+    """A new B allocated where a freed B lived, with the same shape and version counter,
+    must be packed again (the cache holds only a weak reference to the packed tensor)."""
+    M, K, N = 64, 2048, N_OUT
+    a, _, b, _ = _problem(M, K, gpu)
+    out = torch.empty(M, N, dtype=BF16, device=gpu)
+    KO.gemm_launch(a, b, out, None, {}, False, False)
+    torch.cuda.synchronize()
+    first = out.clone()
+    ptr, ver = b.data_ptr(), b._version
+    del b
+    b2 = torch.empty(K, N, dtype=BF16, device=gpu)  # the caching allocator's freed block
+    assert b2.data_ptr() == ptr
+    b2.copy_((torch.randn(K, N, device=gpu) * 0.02).to(BF16))
+    while b2._version < ver:
+        b2.add_(0.0)
+    if b2._version != ver:
+        pytest.skip("could not match the freed tensor's version counter")
+    KO.gemm_launch(a, b2, out, None, {}, False, False)
+    torch.cuda.synchronize()
+    assert not torch.equal(out, first)
+    torch.testing.assert_close(out.float(), a.float() @ b2.float(), rtol=1e-2, atol=1e-2)

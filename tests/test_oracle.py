@@ -577,3 +577,51 @@ def test_down_merge_atomic_closed_forms():
     tm = O.down_token_major(a, w2, tw, ids, r)
     bound = 5 * 2.0 ** -8 * (at.float().abs() + 4 * r.float().abs().max()) + 1e-3
     assert ((at.float() - tm.float()).abs() <= bound).all()
+
+
+def test_moe_mlp_rows_equals_moe_mlp():
+    """`moe_mlp_rows` over every row is `moe_mlp` before its bf16 round, bit for bit (and so
+    the reference's golden routed output); over a subset it gives the same rows."""
+    g = np.load(GOLD / "tiny_moe.npz")
+    d = _tiny()
+    _, tw, ti = O.router_reference(d["x"], d["gate"], None, topk=4)
+    T = d["x"].shape[0]
+    full = O.moe_mlp_rows(d["x"], d["w13"], d["w2"], tw, ti, list(range(T)))
+    assert full.dtype == torch.float32
+    assert np.array_equal(u16(full.to(BF16)), g["routed"])
+    assert torch.equal(full.to(BF16), O.moe_mlp(d["x"], d["w13"], d["w2"], tw, ti))
+    rows = [0, 3, 7, 15]
+    sub = O.moe_mlp_rows(d["x"], d["w13"], d["w2"], tw, ti, rows)
+    torch.testing.assert_close(sub, full[rows], rtol=1e-6, atol=1e-6)
+
+
+def test_block_reference_vs_fp64_composition():
+    """`block_reference` = bf16(routed + h + shared) against the same composition in
+    fp64 (textbook GEMMs, exact SwiGLU, no intermediate rounding); with the shared
+    weights zeroed it drops to bf16(moe_mlp + h), so a dropped or doubled term fails."""
+    d = _tiny()
+    _, tw, ti = O.router_reference(d["x"], d["gate"], None, topk=4)
+    x, h = d["x"], d["act_in"][:, : d["x"].shape[1]].contiguous()
+    got = O.block_reference(h, x, d["w13"], d["w2"], d["w13s"], d["w2s"], tw, ti)
+    xd, hd = x.double().numpy(), h.double().numpy()
+    w13, w2 = d["w13"].double().numpy(), d["w2"].double().numpy()
+    w13s, w2s = d["w13s"][0].double().numpy(), d["w2s"][0].double().numpy()
+    I = w2.shape[2]
+    silu = lambda v: v / (1 + np.exp(-v))
+    want = hd.copy()
+    for t in range(xd.shape[0]):
+        for j in range(ti.shape[1]):
+            e = int(ti[t, j])
+            g_ = w13[e] @ xd[t]
+            want[t] += float(tw[t, j]) * (w2[e] @ (silu(g_[:I]) * g_[I:]))
+        gs = w13s @ xd[t]
+        want[t] += w2s @ (silu(gs[:I]) * gs[I:])
+    err = np.abs(got.double().numpy() - want).max() / np.abs(want).max()
+    assert err < 1e-2
+    # the shared term is not negligible here, and zeroing it gives bf16(routed + h)
+    shared_only = want - hd
+    assert np.abs(shared_only).max() > 0.05 * np.abs(want).max()
+    z13, z2 = torch.zeros_like(d["w13s"]), torch.zeros_like(d["w2s"])
+    no_sh = O.block_reference(h, x, d["w13"], d["w2"], z13, z2, tw, ti)
+    routed = O.moe_mlp(x, d["w13"], d["w2"], tw, ti)
+    assert torch.equal(no_sh, (routed.float() + h.float()).to(BF16))
