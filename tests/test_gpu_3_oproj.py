@@ -111,23 +111,24 @@ def test_oproj_rejects_wrong_output_dtype(gpu):
 
 
 def test_oproj_pack_cache_misses_a_new_weight_at_a_freed_address(gpu):
-    """A new B allocated where a freed B lived, with the same shape and version counter,
-    must be packed again (the cache holds only a weak reference to the packed tensor)."""
+    """A new B tensor at the address of a B that is gone, with the same shape, strides and
+    version counter but other values, must be packed again: the cache holds only a weak
+    reference to the tensor it packed.  (`.data` gives tensors over one memory block with
+    version counters of their own, so the address and version collide by construction.)"""
     M, K, N = 64, 2048, N_OUT
-    a, _, b, _ = _problem(M, K, gpu)
+    a, _, b0, _ = _problem(M, K, gpu)
+    b = torch.empty(K, N, dtype=BF16, device=gpu)
+    b.data.copy_(b0)  # b._version stays 0
     out = torch.empty(M, N, dtype=BF16, device=gpu)
     KO.gemm_launch(a, b, out, None, {}, False, False)
     torch.cuda.synchronize()
     first = out.clone()
     ptr, ver = b.data_ptr(), b._version
+    keep = b.data  # the memory block lives on under another tensor
     del b
-    b2 = torch.empty(K, N, dtype=BF16, device=gpu)  # the caching allocator's freed block
-    assert b2.data_ptr() == ptr
-    b2.copy_((torch.randn(K, N, device=gpu) * 0.02).to(BF16))
-    while b2._version < ver:
-        b2.add_(0.0)
-    if b2._version != ver:
-        pytest.skip("could not match the freed tensor's version counter")
+    b2 = keep.view(K, N)
+    b2.data.copy_((torch.randn(K, N, device=gpu) * 0.02).to(BF16))
+    assert b2.data_ptr() == ptr and b2._version == ver
     KO.gemm_launch(a, b2, out, None, {}, False, False)
     torch.cuda.synchronize()
     assert not torch.equal(out, first)

@@ -17,7 +17,7 @@ BF16 = torch.bfloat16
 
 
 def test_token_major_override_needs_the_streaming_layout(gpu):
-    E, H, I, T = 16, 256, 128, 512
+    E, H, I, T = 16, 512, 256, 512
     w13 = torch.zeros(E, 2 * I, H, dtype=BF16, device=gpu)
     w2 = torch.zeros(E, H, I, dtype=BF16, device=gpu)
     w13s, w2s = w13[:1].clone(), w2[:1].clone()
