@@ -31,6 +31,7 @@ SIGNATURES: dict[str, list] = {
     "glm52_router_topk": [_P, _L, _P, _P, _L, _P, _L, _I, _I, _I, _F, _I, _P],
     "glm52_moe_align": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "glm52_moe_align_ws": [_P, _I, _I, _I, _I, _P, _P, _P, _P, _L, _P],
+    "glm52_moe_align_noalloc": [_P, _I, _I, _I, _I, _P, _P, _P, _P],
     "glm52_decode_front": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L,
                            _I, _I, _I, _I, _F, _F, _I, _I, _I, _P, _P, _P, _P, _P],
     "glm52_decode_norm_logits": [_P, _L, _P, _L, _P, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I,

@@ -36,6 +36,8 @@
 // the ids in LDS and builds the layout from them.
 #include "select.h"
 
+#include <mutex>
+
 using namespace glm52;
 
 namespace {
@@ -258,6 +260,60 @@ extern "C" int glm52_moe_align_ws(const int32_t* topk_ids, int numel, int block_
                                                         capacity, hist, sorted_token_ids,
                                                         expert_ids, num_tokens_post_padded);
   GLM52_RETURN_LAUNCH();
+}
+
+// ------------------------------------------------------------------------------------
+// glm52_moe_align_noalloc: glm52_moe_align_ws with its chunk histograms in a scratch array
+// of the library's own, for callers that cannot allocate.  The array holds the histograms
+// of up to kMaxChunks chunks of kMaxE experts (512 KB); each GPU the library runs on holds
+// its own copy until the process ends.  Host code never passes the array's name (a host
+// stand-in) to a kernel: the first call on a device, with that device current, looks up
+// the device copy's address once and keeps it per device.  align_hist_kernel writes every
+// (chunk, expert) entry it later reads, so nothing needs clearing between calls; calls
+// that overlap on one GPU share the array and race.
+// ------------------------------------------------------------------------------------
+static __device__ __align__(256) int32_t scratch[kMaxChunks * kMaxE];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// the current device's copy of `scratch` (looked up on the first call on that device)
+int scratch_of_current_device(void** out) {
+  int dev = -1;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return (int)err;
+  if (dev < 0 || dev >= kMaxDevices) return GLM52_EUNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return (int)err;
+    if (!p) return GLM52_EUNSUPPORTED;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return GLM52_OK;
+}
+}  // namespace
+
+extern "C" int glm52_moe_align_noalloc(const int32_t* topk_ids, int numel, int block_m,
+                                       int num_experts, int capacity, int32_t* sorted_token_ids,
+                                       int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                                       hipStream_t stream) {
+  if (numel < 0 || numel > kMaxChunks * kChunkIds || num_experts <= 0 || num_experts > kMaxE)
+    return GLM52_EINVAL;
+  const int64_t need = chunk_hist_bytes(numel, num_experts);
+  if (need == 0)  // one chunk or less: the single-workgroup build, which needs no scratch
+    return glm52_moe_align(topk_ids, numel, block_m, num_experts, capacity, sorted_token_ids,
+                           expert_ids, num_tokens_post_padded, stream);
+  if (need > (int64_t)sizeof(scratch)) return GLM52_EINVAL;
+  void* ws = nullptr;
+  const int rc = scratch_of_current_device(&ws);
+  if (rc != GLM52_OK) return rc;
+  return glm52_moe_align_ws(topk_ids, numel, block_m, num_experts, capacity, sorted_token_ids,
+                            expert_ids, num_tokens_post_padded, ws, need, stream);
 }
 
 extern "C" int glm52_router_topk_align(const float* logits, int64_t stride_l, const float* bias,

@@ -86,6 +86,18 @@ int glm52_moe_align_ws(const int32_t* topk_ids, int numel, int block_m, int num_
                        int32_t* num_tokens_post_padded, void* workspace,
                        int64_t workspace_bytes, hipStream_t stream);
 
+/* glm52_moe_align_ws with no workspace argument and no allocation: the chunk histograms
+ * live in a scratch array of the library's own (512 KB per GPU, held until the process
+ * ends), whose device address the first call on each device looks up with that device
+ * current.  Same outputs, bit for bit.  numel <= 1048576 and num_experts <= 256, else
+ * GLM52_EINVAL with nothing launched.  Calls that overlap on one GPU share the scratch and
+ * race; the stream must belong to the current device.  No counterpart in the reference:
+ * it is for callers that cannot allocate (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int glm52_moe_align_noalloc(const int32_t* topk_ids, int numel, int block_m, int num_experts,
+                            int capacity, int32_t* sorted_token_ids, int32_t* expert_ids,
+                            int32_t* num_tokens_post_padded, hipStream_t stream);
+
 /* glm52_router_topk followed by glm52_moe_align in one single-workgroup launch, for
  * decode (T * topk <= 256).  Replaces the topk_only + moe_align_block_size pair
  * (glm52/kernels/norm_router.py:352-354, glm52/reference.py:85-128). */
