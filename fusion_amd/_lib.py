@@ -70,6 +70,7 @@ SIGNATURES: dict[str, list] = {
 # name -> (argument types, return type) for entry points that do not return a status
 QUERIES: dict[str, tuple[list, type]] = {
     "glm52_router_workspace_bytes": ([_I, _I, _I], c_int64),
+    "glm52_router_select_workspace_bytes": ([_I, _I, _I], c_int64),
     "glm52_moe_align_workspace_bytes": ([_I, _I], c_int64),
     "glm52_packed_w512_bytes": ([_I, _I, _I, _I], c_int64),
     "glm52_oproj_workspace_bytes": ([_I, _I, _I], c_int64),

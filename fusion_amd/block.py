@@ -23,7 +23,7 @@ the routing computed live instead of frozen, and the tail fused):
                                  over all experts, one rounding -- the reference's
                                  token-major strategy #9(b))
 
-At block sizes 64 and 128 (prefill) the four GEMMs read weights packed once in the
+At block sizes 64, 128 and 256 (prefill) the four GEMMs read weights packed once in the
 constructor (`pack_w512`: every 32-k stage of a 512-row W tile as 32 KB of contiguous
 memory), which computes the same bits as reading them in place.
 
@@ -49,17 +49,23 @@ from .kernels.moe_gateup import moe_gemm, moe_gemm_packed, moe_gemm_shared, pack
 
 BF16 = torch.bfloat16
 
+# token count from which the router runs the bounded bf16 logits on the gate rows
+BOUNDED_ROUTER_MIN_T = 1024
+
 
 def default_block_m(T: int) -> int:
     """Layout block size per regime: 16-row slices stream weights while each expert sees
     a handful of rows; 64- or 128-row blocks of the wide LDS-tiled mapping once rows per
-    expert reach the tens, so each expert's W is fetched by as few blocks as possible."""
+    expert reach the tens, and 256-row blocks (256 x 256 tiles) once they pass a hundred,
+    so that most experts' rows fit one block and each W tile is streamed by one workgroup."""
     rows_per_expert = T * C.TOPK / C.E
     if rows_per_expert <= 12:
         return 16
     if rows_per_expert <= 48:
         return 64
-    return 128
+    if rows_per_expert <= 100:
+        return 128
+    return 256
 
 
 def default_shared_block_m(T: int) -> int:
@@ -138,16 +144,18 @@ class MoEBlock:
             # weight-streaming w13 launch (block size 16) writes before the tail
             raise ValueError("token_major needs the weight-streaming layout (block size 16, "
                              f"T <= 384); T={T} runs block size {self.bm}")
-        self.gate_rows = wgt.t().contiguous() if self.decode else None  # [E, H]
-        self.wgt_rows = self.gate_rows.t() if self.decode else None  # its [H, E] view
-        need = KR.workspace_bytes(T, H, E)
+        # the gate as rows [E, H]: decode streams a wave per row; above, the router runs
+        # the bounded bf16 logits with the exact rule on each token's candidates
+        self.gate_rows = wgt.t().contiguous()
+        self.wgt_rows = self.gate_rows.t()  # its [H, E] view
+        need = max(KR.workspace_bytes(T, H, E), KR.select_workspace_bytes(T, H, E))
         self.router_ws = torch.empty(max(need, 8), dtype=torch.uint8, device=dev)
         self.cfg_topk = {"correction_bias": bias, "scale": scale, "workspace": self.router_ws}
         self.graph = None
-        # prefill (block sizes 64 and 128): the GEMMs read weights packed once here, every
+        # prefill (block sizes 64, 128, 256): the GEMMs read weights packed once here, every
         # 32-k stage of a 512-row W tile as 32 KB of contiguous memory (the same bits)
         self.packed = (pack and variant is None and not self.shared_fused
-                       and self.bm in (64, 128) and self.sbm in (64, 128))
+                       and self.bm in (64, 128, 256) and self.sbm in (64, 128, 256))
         if self.packed:
             self.w13_p = pack_w512(w13, self.I, self.I, True)
             self.w2_p = pack_w512(w2, self.H, 0, False)
@@ -156,6 +164,7 @@ class MoEBlock:
 
     # ---- the chain -------------------------------------------------------------------
     def front_end(self, x, r):
+        T = self.T
         if self.front_fused:
             # norm + logits here; the routing is derived inside the w13 launch (experts())
             decode_norm_logits_into(x, r, self.w_norm, self.h, self.y, self.gate_rows,
@@ -168,7 +177,10 @@ class MoEBlock:
             topk_align_into(self.logits, self.topw, self.topi, self.cfg_topk, self.bm, self.E,
                             self.sti, self.eids, self.ntp)
         else:
-            KR.router(self.y, self.wgt, self.logits, self.topw, self.topi, self.cfg_topk)
+            # from ~1k tokens the bounded bf16 router on the gate rows; below, the fp64
+            # MFMA router on the [H, E] gate is the faster of the two (same ids, weights)
+            gw = self.wgt_rows if T >= BOUNDED_ROUTER_MIN_T else self.wgt
+            KR.router(self.y, gw, self.logits, self.topw, self.topi, self.cfg_topk)
             moe_align_block_size_into(self.topi, self.bm, self.E, self.sti, self.eids, self.ntp,
                                       self.align_ws)
 

@@ -44,13 +44,7 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library; raises on failure."""
-    srcs = sources()
-    if not srcs:
-        raise RuntimeError(f"no HIP sources under {CSRC}")
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(CSRC), "-o", str(tmp), *map(str, srcs)]
+def _run(cmd: list[str], verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -60,6 +54,29 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{err}")
     if verbose and err.strip():
         print(err, file=sys.stderr)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every HIP source (one hipcc per file, in parallel) and link them into one
+    shared library; raises on failure.  The sources share no device code, so each object
+    carries its own gfx950 code object."""
+    import tempfile
+    from concurrent.futures import ThreadPoolExecutor
+
+    srcs = sources()
+    if not srcs:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    compile_flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    jobs = max(1, min(len(srcs), len(os.sched_getaffinity(0)), 16))
+    with tempfile.TemporaryDirectory(prefix="glm52_build_") as tmpdir:
+        objs = [Path(tmpdir) / (src.stem + ".o") for src in srcs]
+        with ThreadPoolExecutor(jobs) as pool:
+            list(pool.map(lambda so: _run([hipcc(), *compile_flags, "-c", "-I", str(CSRC),
+                                           "-o", str(so[1]), str(so[0])], verbose),
+                          zip(srcs, objs)))
+        tmp = LIB.with_suffix(".so.tmp")
+        _run([hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
+              *map(str, objs)], verbose)
     os.replace(tmp, LIB)
     return LIB
 

@@ -373,7 +373,8 @@ int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
 // variant: 0 = choose (stream when BM == 16; 512-row W tiles when BM is 64 or 128, else the
 // 256-row wide mapping for shapes the 512-row one does not cover; tiled otherwise),
 // 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages, 5 = 512-row
-// W tiles (moe_gemm_wide.hip; block_m in {64, 128}), 6 = contiguous-run weight stream
+// W tiles (moe_gemm_wide.hip; block_m in {64, 128}; 256 runs 256 x 256 tiles), 6 =
+// contiguous-run weight stream
 // (moe_gemm_runs.hip; block_m 16).  The default for block_m 16 is 6, else 1.
 extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                               int64_t stride_we, int64_t stride_wn, int gate_up_offset,
@@ -397,7 +398,7 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
              num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
              nullptr, 0, nullptr, nullptr, 0, 0, a_bytes(num_valid_tokens, a_row_div, stride_am, k), 0};
   const bool weighted = topk_weights != nullptr;
-  const bool auto_wide = variant == 0 && (block_m == 64 || block_m == 128);
+  const bool auto_wide = variant == 0 && (block_m == 64 || block_m == 128 || block_m == 256);
   if (variant == 5 || auto_wide) {
     // the 512-row mapping addresses token rows with 32-bit byte offsets; shapes it has no
     // instance for fall back to the 256-row mapping when the mapping was not forced
@@ -474,7 +475,8 @@ extern "C" int glm52_moe_down_merge(const void* a, int64_t stride_am, const void
       (reinterpret_cast<uintptr_t>(out) & 3u) || (stride_om % 2) || stride_om < n_out ||
       (w_packed && !al16(w_packed)))
     return GLM52_EINVAL;
-  if (block_m != 16 && block_m != 64 && block_m != 128) return GLM52_EUNSUPPORTED;
+  if (block_m != 16 && block_m != 64 && block_m != 128 && block_m != 256)
+    return GLM52_EUNSUPPORTED;
   if (capacity % block_m) return GLM52_EINVAL;
   if (capacity == 0) return GLM52_OK;
   GemmArgs g{static_cast<const uint16_t*>(a), stride_am, 1, static_cast<const uint16_t*>(w),
@@ -501,7 +503,8 @@ extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row
                                      int gated, hipStream_t stream) {
   if (!a || !w_packed || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
     return GLM52_EINVAL;
-  if ((block_m != 64 && block_m != 128) || capacity < 0 || (capacity % block_m) != 0)
+  if ((block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
+      (capacity % block_m) != 0)
     return GLM52_EINVAL;
   if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 || (k % 64) != 0 ||
       a_row_div <= 0)

@@ -349,31 +349,47 @@ GLM52_DEV int w512_chunk(int l) { return (l & 3) ^ (((l >> 2) >> 2) & 3); }
 
 // EPI (non-gated): 0 bf16 store; 1 bf16(acc + R); 2 C32 += acc (+ R); 3 C32 = acc (fp32
 // partials); 4 the atomic expert merge, bf16 packed atomic adds into row tok / merge_topk.
-template <int MT, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
+//
+// NTW = 512: the tile above (4 waves along W, each 128 W rows x all MT tokens).
+// NTW = 256 (MT = 256): a 256-token x 256-row tile, the waves 2 x 2 (wave (wn, wm): W rows
+// wn * 128 .. +127 against tokens wm * 128 .. +127).  Its W tile is half of a 512-row tile
+// -- gated: `gate` and `up` rows of 128 consecutive outputs -- which the packed layout
+// keeps as 16 KB of contiguous memory per stage (512-row waves 2s and 2s + 1), so both
+// tile heights read one packed copy.  A stage is 32 KB, so five fit in LDS: four in flight
+// while one is multiplied.  A tile of 256 tokens covers most experts' rows at prefill
+// sizes in one item, so most W tiles are streamed by one workgroup only.
+template <int MT, int NTW, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
-  constexpr int NTW = 512;         // W rows per tile
   constexpr int BKS = 32;          // k per stage
-  constexpr int NSTAGE = 4;
+  constexpr int WN = NTW / 128;    // waves along W
+  constexpr int WM = 4 / WN;       // waves along the tokens
+  constexpr int TPW = MT / WM;     // tokens per wave
   constexpr int RPI = 16;          // staged rows per load instruction (64 lanes x 16 B / 64 B)
-  constexpr int TF = MT / 32;      // token blocks of 32
+  constexpr int TF = TPW / 32;     // token blocks of 32 per wave
   constexpr int NO = GATED ? NTW / 2 : NTW;
-  constexpr int WI = NTW / RPI / 4;  // W load instructions per wave and stage (8)
+  constexpr int NO512 = GATED ? 256 : 512;  // outputs of a packed 512-row tile
+  constexpr int SPLIT = 512 / NTW;          // W tiles per packed 512-row tile
+  constexpr int WI = NTW / RPI / 4;  // W load instructions per wave and stage
   constexpr int AI = MT / RPI / 4;   // token-row load instructions per wave and stage
   constexpr int IPS = WI + AI;
   constexpr int SROWS = NTW + MT;
   constexpr int SELEM = SROWS * BKS;  // elements per stage
-  static_assert(AI >= 1 && TF >= 1 && IPS < 64, "stage shape");
+  constexpr int NSTAGE = 5 * SELEM * 2 <= 163840 ? 5 : 4;
+  static_assert(WN * WM == 4 && AI >= 1 && TF >= 1 && TF <= 4, "tile");
+  static_assert((NSTAGE - 2) * IPS < 64, "vmcnt range");
   __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wv = tid / kWave;
   const int wvu = __builtin_amdgcn_readfirstlane(wv);
+  const int wn = wvu % WN, wm = wvu / WN;
   const int l32 = lane % 32, h = lane / 32;
 
   const int ntp = *p.ntp;
   const int num_m = ntp / MT;
   const int num_n = p.n_out / NO;
+  const int num_n512 = p.n_out / NO512;
   const int items = num_m * num_n;
   const int nk = p.K / BKS;
   const int per_xcd = (items + 7) / 8;
@@ -404,6 +420,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     if (p.sti[row0] >= p.num_valid) continue;
     const int e = p.eids[pid_m];
     const int n0 = pid_n * NO;
+    const int P = pid_n / SPLIT, sub = pid_n % SPLIT;  // the packed 512-row tile and half
 
     // real tokens fill a prefix of the block: every wave counts them (no LDS, no barrier)
     int nv_rows = 0;
@@ -411,12 +428,13 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     for (int q = 0; q < MT; q += kWave)
       nv_rows += __popcll(__ballot(q + lane < MT && p.sti[row0 + q + lane] < p.num_valid));
     nv_rows = __builtin_amdgcn_readfirstlane(nv_rows);
-    const int nvf = __builtin_amdgcn_readfirstlane(min(TF, (nv_rows + 31) / 32));
+    const int nvf = __builtin_amdgcn_readfirstlane(max(0, min(TF, (nv_rows - wm * TPW + 31) / 32)));
 
-    // W load instruction i of the wave fills slab rows i*16 .. +15: W rows
-    // wrow(i) + phi32(lane / 4) (wrow(i) wave-uniform), 16 bytes at logical chunk dc each;
-    // the lane's byte offsets inside W[e] (< 2^32: an expert's W is far smaller)
-    const uint16_t* wexp = PACKED ? p.Wp + (int64_t)(e * num_n + pid_n) * nk * (kPackStage / 2)
+    // W load instruction i of the wave fills slab rows (wv * WI + i) * 16 .. +15 of the
+    // tile: packed, 1 KB of contiguous memory; in place, W rows wrow + phi32(lane / 4), 16
+    // bytes at logical chunk dc each (the lane's byte offsets inside W[e], < 2^32)
+    const uint16_t* wexp = PACKED ? p.Wp + ((int64_t)(e * num_n512 + P) * nk * SPLIT + sub) *
+                                               (kPackStage / 2 / SPLIT)
                                   : p.W + (int64_t)e * p.swe;
     uint32_t wvoff[WI];
 #pragma unroll
@@ -424,7 +442,8 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       if (PACKED) {
         wvoff[i] = (uint32_t)((wv * WI + i) * 1024 + lane * 16);
       } else {
-        const int row = n0 + w512_row(GATED, p.gu_off, wv, i, lane);
+        const int slab = sub * (NTW / RPI) + wv * WI + i;  // 1 KB slab of the 512-row tile
+        const int row = P * NO512 + w512_row(GATED, p.gu_off, slab / 8, slab % 8, lane);
         wvoff[i] = (uint32_t)(((int64_t)row * p.swn + dc * 8) * 2);
       }
     }
@@ -442,7 +461,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
         const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * (kPackStage / 2) : wexp + kc;
-        dma16s(src, wvoff[i], sb + (uint32_t)((wvu * 128 + i * RPI) * BKS * 2));
+        dma16s(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
       } else {
         const int j = i - WI;
         dma16s(p.A + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
@@ -451,6 +470,23 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 
     auto run = [&](auto nv_tag) {
       constexpr int NV = decltype(nv_tag)::value;
+      if constexpr (NV == 0) {
+        // no real token in this wave's rows: it still stages its share of every stage
+#pragma unroll
+        for (int st = 0; st < NSTAGE - 1; ++st)
+#pragma unroll
+          for (int i = 0; i < IPS; ++i) issue_one(i, st);
+        GLM52_WAIT_VMCNT((NSTAGE - 2) * IPS);
+        __syncthreads();
+#pragma unroll 1
+        for (int kt = 0; kt < nk; ++kt) {
+          GLM52_WAIT_VMCNT((NSTAGE - 3) * IPS);
+          __syncthreads();
+#pragma unroll
+          for (int i = 0; i < IPS; ++i) issue_one(i, kt + NSTAGE - 1);
+        }
+        return;
+      } else {
       constexpr int NMF = 8 * NV;           // MFMAs per stage
       constexpr int NRD = 8 + 2 * NV;       // fragment reads per stage
       constexpr int NOPS = NRD + IPS;       // reads and loads spread over the MFMAs
@@ -467,27 +503,27 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       auto read_op = [&](int q, const uint16_t* sb, uint4 (&dw)[2][4], uint4 (&da)[2][NV]) {
         if (q < 8) {
           const int ks = q / 4, f = q % 4;
-          dw[ks][f] = *reinterpret_cast<const uint4*>(sb + (wv * 128 + f * 32) * BKS + (ks ? rd1 : rd0));
+          dw[ks][f] = *reinterpret_cast<const uint4*>(sb + (wn * 128 + f * 32) * BKS + (ks ? rd1 : rd0));
         } else {
           const int ks = (q - 8) / NV, t = (q - 8) % NV;
-          da[ks][t] = *reinterpret_cast<const uint4*>(sb + (NTW + t * 32) * BKS + (ks ? rd1 : rd0));
+          da[ks][t] = *reinterpret_cast<const uint4*>(sb + (NTW + wm * TPW + t * 32) * BKS + (ks ? rd1 : rd0));
         }
       };
 
       // one stage: the MFMAs of stage kt on fragments [P], interleaved with the reads of
-      // stage kt+1 into fragments [1-P] and the loads of stage kt+3
+      // stage kt+1 into fragments [1-P] and the loads of stage kt+NSTAGE-1
       auto stage = [&](int kt, auto par_tag) {
-        constexpr int P = decltype(par_tag)::value;
-        // stage kt+1 landed for this wave (stage kt+2 may still be in flight) and for
+        constexpr int PAR = decltype(par_tag)::value;
+        // stage kt+1 landed for this wave (later stages may still be in flight) and for
         // every wave; every wave is done with the buffer refilled in this stage
-        GLM52_WAIT_VMCNT(IPS);
+        GLM52_WAIT_VMCNT((NSTAGE - 3) * IPS);
         __syncthreads();
         const uint16_t* sbn = ring + ((kt + 1) % NSTAGE) * SELEM;
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int m = 0; m < NMF; ++m) {
           const int ks = m / (4 * NV), f = (m / NV) % 4, t = m % NV;
-          acc[f][t] = mfma32(fw[P][ks][f], fa[P][ks][t], acc[f][t]);
+          acc[f][t] = mfma32(fw[PAR][ks][f], fa[PAR][ks][t], acc[f][t]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int o = 0; o < NOPS; ++o) {
@@ -497,19 +533,19 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
               const bool is_load = o < both ? (o % 2) == 0 : IPS > NRD;
               const int idx = o < both ? o / 2 : both / 2 + (o - both);
               if (is_load) issue_one(idx, kt + NSTAGE - 1);
-              else read_op(idx, sbn, fw[1 - P], fa[1 - P]);
+              else read_op(idx, sbn, fw[1 - PAR], fa[1 - PAR]);
               __builtin_amdgcn_sched_barrier(0);
             }
           }
         }
       };
 
-      // prologue: stages 0 .. 2 in flight; stage 0 landed everywhere; its fragments read
+      // prologue: stages 0 .. NSTAGE-2 in flight; stage 0 landed everywhere; its fragments read
 #pragma unroll
       for (int st = 0; st < NSTAGE - 1; ++st)
 #pragma unroll
         for (int i = 0; i < IPS; ++i) issue_one(i, st);
-      GLM52_WAIT_VMCNT(2 * IPS);
+      GLM52_WAIT_VMCNT((NSTAGE - 2) * IPS);
       __syncthreads();
 #pragma unroll
       for (int q = 0; q < NRD; ++q) read_op(q, ring, fw[0], fa[0]);
@@ -522,7 +558,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
-        const int tok = p.sti[row0 + t * 32 + l32];
+        const int tok = p.sti[row0 + wm * TPW + t * 32 + l32];
         if (tok >= p.num_valid) continue;
         uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;  // EPI 0, 1
         if (GATED) {
@@ -531,7 +567,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = silu_mul(acc[fp][t][i], acc[fp + 2][t][i]);
-            uint16_t* dst = crow + n0 + wv * 64 + fp * 32 + h * 16;
+            uint16_t* dst = crow + n0 + wn * 64 + fp * 32 + h * 16;
             *reinterpret_cast<uint4*>(dst) = pack8(v);
             *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
           }
@@ -543,7 +579,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
             float v[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
-            const int col = n0 + wv * 128 + f * 32 + h * 16;
+            const int col = n0 + wn * 128 + f * 32 + h * 16;
             if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
               const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
               float rf[16];
@@ -580,8 +616,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
           }
         }
       }
+      }
     };
     switch (nvf) {
+      case 0: run(std::integral_constant<int, 0>{}); break;
       case 1: run(std::integral_constant<int, 1>{}); break;
       case 2: run(std::integral_constant<int, (TF >= 2 ? 2 : 1)>{}); break;
       case 3: run(std::integral_constant<int, (TF >= 3 ? 3 : 1)>{}); break;
@@ -591,25 +629,25 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   }
 }
 
-template <int MT, bool GATED, bool WEIGHTED>
+template <int MT, int NTW, bool GATED, bool WEIGHTED>
 int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
-  constexpr int NO = GATED ? 256 : 512;
-  if ((a.n_out % NO) || (a.K % 64)) return GLM52_EUNSUPPORTED;
+  constexpr int NO = GATED ? NTW / 2 : NTW;
+  if ((a.n_out % (GATED ? 256 : 512)) || (a.K % 64)) return GLM52_EUNSUPPORTED;
   const int items_max = (capacity / MT) * (a.n_out / NO);
   int grid = items_max < 256 ? items_max : 256;
   grid = ((grid + 7) / 8) * 8;
   if constexpr (!GATED && !WEIGHTED) {
     if (a.epi != 0 && !a.Wp) return GLM52_EUNSUPPORTED;
     if (a.epi == 1) {
-      moe_gemm_w512_kernel<MT, false, false, true, 1><<<grid, 256, 0, st>>>(a);
+      moe_gemm_w512_kernel<MT, NTW, false, false, true, 1><<<grid, 256, 0, st>>>(a);
       GLM52_RETURN_LAUNCH();
     }
     if (a.epi == 2) {
-      moe_gemm_w512_kernel<MT, false, false, true, 2><<<grid, 256, 0, st>>>(a);
+      moe_gemm_w512_kernel<MT, NTW, false, false, true, 2><<<grid, 256, 0, st>>>(a);
       GLM52_RETURN_LAUNCH();
     }
     if (a.epi == 3) {
-      moe_gemm_w512_kernel<MT, false, false, true, 3><<<grid, 256, 0, st>>>(a);
+      moe_gemm_w512_kernel<MT, NTW, false, false, true, 3><<<grid, 256, 0, st>>>(a);
       GLM52_RETURN_LAUNCH();
     }
   } else {
@@ -618,26 +656,27 @@ int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
   if (a.merge_topk > 0) {  // the atomic expert merge: weighted w2 only
     if constexpr (!GATED && WEIGHTED) {
       if (a.Wp)
-        moe_gemm_w512_kernel<MT, false, true, true, 4><<<grid, 256, 0, st>>>(a);
+        moe_gemm_w512_kernel<MT, NTW, false, true, true, 4><<<grid, 256, 0, st>>>(a);
       else
-        moe_gemm_w512_kernel<MT, false, true, false, 4><<<grid, 256, 0, st>>>(a);
+        moe_gemm_w512_kernel<MT, NTW, false, true, false, 4><<<grid, 256, 0, st>>>(a);
       GLM52_RETURN_LAUNCH();
     } else {
       return GLM52_EUNSUPPORTED;
     }
   }
   if (a.Wp)
-    moe_gemm_w512_kernel<MT, GATED, WEIGHTED, true><<<grid, 256, 0, st>>>(a);
+    moe_gemm_w512_kernel<MT, NTW, GATED, WEIGHTED, true><<<grid, 256, 0, st>>>(a);
   else
-    moe_gemm_w512_kernel<MT, GATED, WEIGHTED, false><<<grid, 256, 0, st>>>(a);
+    moe_gemm_w512_kernel<MT, NTW, GATED, WEIGHTED, false><<<grid, 256, 0, st>>>(a);
   GLM52_RETURN_LAUNCH();
 }
 
 template <bool GATED, bool WEIGHTED>
 int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
   switch (a.BM) {
-    case 64: return launch_w512<64, GATED, WEIGHTED>(a, capacity, st);
-    case 128: return launch_w512<128, GATED, WEIGHTED>(a, capacity, st);
+    case 64: return launch_w512<64, 512, GATED, WEIGHTED>(a, capacity, st);
+    case 128: return launch_w512<128, 512, GATED, WEIGHTED>(a, capacity, st);
+    case 256: return launch_w512<256, 256, GATED, WEIGHTED>(a, capacity, st);
     default: return GLM52_EUNSUPPORTED;
   }
 }

@@ -350,6 +350,24 @@ int choose_ks(int T, int H) {
 
 }  // namespace
 
+namespace glm52 {
+// router_select.hip: the bf16-MFMA logits with an error bound and the exact rule on the
+// candidates, for T > 16 tokens on the gate's rows
+int64_t router_select_workspace_bytes(int T, int H, int E);
+int launch_router_select(const uint16_t* y, int64_t sy, const uint16_t* gate, int64_t sg,
+                         float* logits, int64_t sl, void* workspace, int64_t workspace_bytes,
+                         const float* bias, float* topw, int64_t stw, int32_t* topi, int64_t sti,
+                         int T, int H, int E, int topk, float scale, int norm_prob,
+                         hipStream_t st);
+}  // namespace glm52
+
+// Above this many tokens glm52_router on the gate's rows takes the bounded bf16 path.
+constexpr int kSelectMinT = 17;
+
+extern "C" int64_t glm52_router_select_workspace_bytes(int T, int H, int E) {
+  return T >= kSelectMinT ? router_select_workspace_bytes(T, H, E) : 0;
+}
+
 extern "C" int64_t glm52_router_workspace_bytes(int T, int H, int E) {
   const int ks = choose_ks(T, H);
   return ks == 1 ? 0 : (int64_t)ks * T * E * (int64_t)sizeof(double);
@@ -459,6 +477,18 @@ extern "C" int glm52_router(const void* y, int64_t stride_y, const void* wgt, in
   if (topk <= 0 || topk > 8 || topk > E || (E % 4) != 0 || !topw || !topi || stride_w < topk ||
       stride_i < topk)
     return GLM52_EINVAL;
+  if (stride_wk == 1 && !wg_is_f32 && T >= kSelectMinT) {
+    // gate rows, many tokens: bf16 MFMA logits, the exact rule on each token's candidates
+    if (T < 0 || H <= 0 || E <= 0 || E > EMAX || !y || !wgt || !logits || stride_l < E ||
+        stride_y < H || (stride_y % 8) || (reinterpret_cast<uintptr_t>(y) & 15u))
+      return GLM52_EINVAL;
+    const int rc = launch_router_select(static_cast<const uint16_t*>(y), stride_y,
+                                        static_cast<const uint16_t*>(wgt), stride_we, logits,
+                                        stride_l, workspace, workspace_bytes, bias, topw,
+                                        stride_w, topi, stride_i, T, H, E, topk, scale, norm_prob,
+                                        stream);
+    if (rc != GLM52_EUNSUPPORTED) return rc;
+  }
   int ks = 1;
   int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
                          workspace, workspace_bytes, T, H, E, &ks, stream);

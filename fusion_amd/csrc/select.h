@@ -81,13 +81,15 @@ GLM52_DEV uint32_t wave_max_u32(uint32_t v) {
 // (key descending, expert index ascending) and writes slot r of sel_s / sel_i.  Each
 // lane keeps its four experts' order keys; a round takes the wave maximum of the lane
 // maxima, finds the lanes that hold it with a ballot and, on a tie between lanes, takes
-// the lowest expert index.  Every lane of the wave must call it.
+// the lowest expert index.  Slot j of a lane whose bit j of `absent` is set takes no
+// part (it is never selected).  Every lane of the wave must call it.
 GLM52_DEV void topk_rank(const float sc[4], const float key[4], int E, int topk, float* sel_s,
-                         int* sel_i) {
+                         int* sel_i, uint32_t absent = 0u) {
   const int lane = threadIdx.x % kWave;
   uint32_t ou[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ou[j] = (lane + j * kWave < E) ? key_order(key[j]) : 0u;
+  for (int j = 0; j < 4; ++j)
+    ou[j] = (lane + j * kWave < E && !((absent >> j) & 1u)) ? key_order(key[j]) : 0u;
   for (int r = 0; r < topk; ++r) {
     // lane-local best: strict > keeps the lower j (the lower expert index) on ties
     uint32_t bu = ou[0];

@@ -173,8 +173,8 @@ def smem_bytes(cfg: dict, fused: bool) -> int:
         return 4 * 32 * 512 * 2 + 4 * 4 * 64 * 4
     if variant == "stream":
         return 8192
-    if variant == "w512" or (variant is None and bm in (64, 128)):
-        return 4 * (512 + bm) * 32 * 2
+    if variant == "w512" or (variant is None and bm in (64, 128, 256)):
+        return 5 * (256 + bm) * 32 * 2 if bm == 256 else 4 * (512 + bm) * 32 * 2
     if variant in ("wide", "wide32"):
         stages, bk = (4, 32) if variant == "wide32" else (3, 64)
         return stages * (256 + bm) * bk * 2 + 4 * bm

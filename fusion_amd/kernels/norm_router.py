@@ -38,8 +38,18 @@ def workspace_bytes(T: int, H: int = HIDDEN, E: int = NUM_EXPERTS) -> int:
     return int(_lib.query("glm52_router_workspace_bytes", T, H, E))
 
 
-def _workspace(T, H, E, device, cfg, wgt=None):
-    need = 0 if (wgt is not None and wgt.stride(0) == 1) else workspace_bytes(T, H, E)
+def select_workspace_bytes(T: int, H: int = HIDDEN, E: int = NUM_EXPERTS) -> int:
+    """Bytes the router (logits + top-k) on the transposed gate view needs at T tokens: the
+    sums of squares behind its error bound, and its K-split partials (0 at T <= 16)."""
+    return int(_lib.query("glm52_router_select_workspace_bytes", T, H, E))
+
+
+def _workspace(T, H, E, device, cfg, wgt=None, select=False):
+    rows = wgt is not None and wgt.stride(0) == 1
+    if rows:
+        need = select_workspace_bytes(T, H, E) if select and wgt.dtype == torch.bfloat16 else 0
+    else:
+        need = workspace_bytes(T, H, E)
     ws = cfg.get("workspace")
     if need and (ws is None or ws.numel() * ws.element_size() < need):
         ws = torch.empty(need, dtype=torch.uint8, device=device)
@@ -75,7 +85,13 @@ def router_gemm(x2, wgt, logits, cfg):
 
 
 def router(x2, wgt, logits, topw, topi, cfg):
-    """router_gemm + topk_only in two launches (split-K partials reduced inside top-k)."""
+    """router_gemm + topk_only in two launches (split-K partials reduced inside top-k).
+
+    With the transposed gate view (`gate.t()`, bf16) and T > 16 the logits run on bf16
+    MFMA with a proven error bound and only each token's candidate experts (those the
+    bound cannot exclude from the top k) get the exact fp64 logit: ids and weights equal
+    the exact rule's bit for bit; `logits` is exact for the candidates (every selected
+    expert among them) and within the bound elsewhere."""
     _check_router_operands(x2, wgt, logits)
     _lib.require_gpu(topw, topi)
     bias = cfg.get("correction_bias")
@@ -85,7 +101,7 @@ def router(x2, wgt, logits, topw, topi, cfg):
     if T == 0:
         return
     E = wgt.shape[1]
-    ws, need = _workspace(T, H, E, x2.device, cfg, wgt)
+    ws, need = _workspace(T, H, E, x2.device, cfg, wgt, select=True)
     _lib.call(
         "glm52_router", _lib.ptr(x2), x2.stride(0), _lib.ptr(wgt), wgt.stride(0), wgt.stride(1),
         int(wgt.dtype == torch.float32), _lib.ptr(logits), logits.stride(0), _lib.ptr(ws), need,

@@ -51,7 +51,14 @@ int64_t glm52_router_workspace_bytes(int T, int H, int E);
 
 /* glm52_router_logits followed by glm52_router_topk in two launches, the split-K
  * reduction folded into the top-k pass.  Replaces the router_gemm + topk_only pair the
- * reference chain launches (glm52/bench/bench_layer.py:426-428). */
+ * reference chain launches (glm52/bench/bench_layer.py:426-428).
+ * On the gate's rows (stride_wk == 1, bf16) and T > 16 the logits run on bf16 MFMA with a
+ * proven error bound, and only each token's candidates -- the experts the bound cannot
+ * exclude from the top k -- get the exact logit: ids and weights equal the exact rule's
+ * bit for bit; logits are exact for the candidates and within the bound elsewhere.  That
+ * path needs glm52_router_select_workspace_bytes(T, H, E) bytes of workspace (16-byte
+ * aligned), H of 4096, 6144 or 8192 (else the exact mappings run), E % 4 == 0. */
+int64_t glm52_router_select_workspace_bytes(int T, int H, int E);
 int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
                  int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
                  void* workspace, int64_t workspace_bytes, const float* bias, float* topw,

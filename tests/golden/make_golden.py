@@ -96,7 +96,7 @@ def main(ref_root: str, what: str = "all") -> None:
 # the token counts and bias kinds of the block's GPU parity cases
 ROUTING_CASES = [(1, "normal"), (4, "zipf"), (16, "normal"), (32, "normal"), (256, "normal"),
                  (2048, "normal"), (8192, "zipf")]
-BLOCK_MS = (16, 64, 128)
+BLOCK_MS = (16, 64, 128, 256)
 
 
 def routing_path(T: int, bias: str) -> Path:
@@ -113,7 +113,7 @@ def routing_fixtures(R) -> None:
     Stored per case: the input digests; the digests of the reference's h and y, and the
     positions and values where its y differs from the order-independent statistic of the
     oracle (`add_rmsnorm_exact`, the device rule) -- so the reference's y is pinned
-    entirely; ids (uint8, E = 256), fp32 weights; for block sizes 16, 64 and 128 the
+    entirely; ids (uint8, E = 256), fp32 weights; for block sizes 16, 64, 128 and 256 the
     digests of sorted_token_ids / expert_ids (int32, exact sizes) and the padded count,
     plus the arrays themselves for T <= 256.
     """

@@ -625,3 +625,78 @@ def test_merge_resadd(gpu, round_mid):
     KM.resadd_only(m, res.to(gpu), out2, {})
     if round_mid:
         assert torch.equal(out2, out)
+
+
+# ------------------------------------------------------------------ router, bounded path
+def select_bound(y_o, gate, logits_exact):
+    """The error bound the bounded router promises for every logit it does not recompute:
+    1.25 * 2^-16 * ||y_t|| ||w_e|| + 2^-21 |L| (plus a hair for the fp32 of L)."""
+    yn = np.sqrt((y_o.double().numpy() ** 2).sum(1))[:, None]
+    wn = np.sqrt((gate.double().numpy() ** 2).sum(1))[None, :]
+    return 1.25 * 2.0 ** -16 * yn * wn + 2.0 ** -20 * np.abs(logits_exact) + 1e-30
+
+
+def run_router_rows(gpu, y, gate, bias, topk=8):
+    T = y.shape[0]
+    E = gate.shape[0]
+    logits = torch.full((T, E), float("nan"), device=gpu)
+    topw = torch.empty(T, topk, dtype=torch.float32, device=gpu)
+    topi = torch.empty(T, topk, dtype=torch.int32, device=gpu)
+    cfg = {"correction_bias": None if bias is None else bias.to(gpu)}
+    KR.router(y.to(gpu), gate.to(gpu).t(), logits, topw, topi, cfg)
+    torch.cuda.synchronize()
+    return logits.cpu().numpy(), topw.cpu().numpy(), topi.cpu().numpy()
+
+
+@pytest.mark.parametrize("T,bias", [(17, "normal"), (100, "zero"), (512, "zipf"),
+                                    (2048, "normal"), (8192, "zipf")])
+def test_router_bounded_path_bitwise(gpu, T, bias):
+    """The gate-rows router above 16 tokens: ids and weights bit for bit against the exact
+    rule; logits exact on every selected expert and within the proven bound elsewhere."""
+    say(f"bounded router T={T} bias={bias}")
+    fe = front_end(T, bias=bias)
+    y_o, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    b = None if bias == "zero" else fe.bias
+    lg, w, ids = run_router_rows(gpu, y_o, fe.gate, b)
+    lg_o, w_o, ids_o = O.router_exact(y_o, fe.wgt, None if b is None else b.numpy())
+    assert np.array_equal(ids, ids_o)
+    assert np.array_equal(w, w_o)
+    sel = np.take_along_axis(lg, ids_o.astype(np.int64), 1)
+    assert np.array_equal(sel, np.take_along_axis(lg_o, ids_o.astype(np.int64), 1))
+    bound = select_bound(y_o, fe.gate, lg_o)
+    ratio = np.abs(lg.astype(np.float64) - lg_o) / bound
+    say(f"  approximate logits: max |error| / bound = {ratio.max():.3e}, "
+        f"exact (recomputed) fraction {(lg == lg_o).mean():.3f}")
+    assert ratio.max() <= 1.0
+
+
+def test_router_bounded_path_ties_and_nan(gpu):
+    """Exact ties above the cut (16 identical gate rows lifted by the bias: the lower
+    indices win), a token of NaN (every key -inf: ids 0..7, NaN weights, as the exact
+    rule) and top-k 6 without normalisation."""
+    T, H, E = 40, 6144, 256
+    fe = front_end(T)
+    y_o, _ = O.add_rmsnorm_exact(fe.x, fe.r, fe.w_norm)
+    gate = fe.gate.clone()
+    gate[3:19] = gate[3]  # experts 3..18 identical
+    bias = torch.zeros(E, dtype=torch.float32)
+    bias[3:19] = 1.0
+    y = y_o.clone()
+    y[5] = float("nan")
+    lg, w, ids = run_router_rows(gpu, y, gate, bias)
+    lg_o, w_o, ids_o = O.router_exact(y, gate.t().contiguous(), bias.numpy())
+    assert np.array_equal(ids, ids_o)
+    assert (ids[:5] == np.arange(3, 11)).all() and (ids[5] == np.arange(8)).all()
+    assert np.array_equal(np.isnan(w), np.isnan(w_o))
+    ok = ~np.isnan(w_o)
+    assert np.array_equal(w[ok], w_o[ok])
+    # top-k 6, unnormalised weights
+    logits = torch.empty(T, E, device=gpu)
+    topw = torch.empty(T, 6, dtype=torch.float32, device=gpu)
+    topi = torch.empty(T, 6, dtype=torch.int32, device=gpu)
+    KR.router(y_o.to(gpu), fe.gate.to(gpu).t(), logits, topw, topi,
+              {"correction_bias": fe.bias.to(gpu), "NORM_PROB": False})
+    lg6 = O.router_logits_exact(y_o, fe.wgt)
+    w6, ids6, _ = O.router_select(lg6, fe.bias.numpy(), 6, norm_prob=False)
+    assert np.array_equal(topi.cpu().numpy(), ids6)
+    assert np.array_equal(topw.cpu().numpy(), w6)

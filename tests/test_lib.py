@@ -100,12 +100,14 @@ def test_shared_layout_matches_reference_rule():
 
 
 def test_default_block_m_regimes():
-    # decode streams 16-row slices; prefill uses the wide tiles' 64- and 128-row blocks
+    # decode streams 16-row slices; prefill uses the wide tiles' 64-, 128- and 256-row blocks
     assert block.default_block_m(1) == 16
     assert block.default_block_m(256) == 16
     assert block.default_block_m(1024) == 64
     assert block.default_block_m(2048) == 128
-    assert block.default_block_m(8192) == 128
+    assert block.default_block_m(3200) == 128
+    assert block.default_block_m(4096) == 256
+    assert block.default_block_m(8192) == 256
     assert [block.default_shared_block_m(T) for T in (1, 32, 256, 2048, 8192)] == [16, 64, 64,
                                                                                     128, 128]
 
@@ -118,3 +120,12 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
         _lib.call("glm52_moe_align", None, 0, 16, 256, 16, None, None, None, None)
     with pytest.raises(RuntimeError, match="not built"):
         _lib.query("glm52_moe_align_workspace_bytes", 65536, 256)
+
+
+def test_router_select_workspace_query():
+    q = lambda t: _lib.query("glm52_router_select_workspace_bytes", t, 6144, 256)  # noqa: E731
+    assert q(16) == 0  # decode keeps the exact rows mapping
+    # 16384 tokens: 256 blocks of 64 tokens, no K split: the gate rows' sums of squares only
+    assert q(16384) == 256 * 4 + 256
+    # 8192 tokens: 128 token blocks x 2 K slices, fp32 partials
+    assert q(8192) == 2 * 256 * 4 + 256 + 2 * 8192 * 256 * 4
