@@ -160,7 +160,7 @@ def main() -> int:
 
         # dominant kernel alone: the block's w13 + SwiGLU launch, events on its stream
         k_ms, _ = timed(blk.w13_step, args.steps, 2)
-        kc = RL.w13_launch(T, n_e, blk.shared_fused, blk.front_fused)
+        kc = RL.w13_launch(T, n_e, blk.shared_fused or blk.packed, blk.front_fused)
         k_us = statistics.mean(k_ms) * 1e3
         roof_us = RL.block_roofline_us(T, n_e)
         med_us = statistics.median(ms) * 1e3
@@ -244,7 +244,9 @@ def w13_kernel_name(blk) -> str:
                 "w13 + SwiGLU)")
     if blk.shared_fused:
         return "moe_gemm_runs_kernel<true, false, false> (routed and shared w13 + SwiGLU)"
-    return f"moe_gemm_w512_kernel<{blk.bm}, true, false> (routed w13 + SwiGLU)"
+    ntw = 256 if blk.bm == 256 else 512
+    return (f"moe_gemm_w512_kernel<{blk.bm}, {ntw}, true, false, true, 0> (routed and shared "
+            f"w13 + SwiGLU)")
 
 
 def hbm_traffic(T: int, timeout_s: float = 240.0) -> dict | None:

@@ -46,6 +46,8 @@ SIGNATURES: dict[str, list] = {
     "glm52_pack_w512": [_P, _L, _L, _I, _I, _I, _I, _I, _P, _P],
     "glm52_moe_gemm_packed": [_P, _L, _I, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I,
                               _P],
+    "glm52_moe_gemm_packed_shared": [_P, _L, _I, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _P, _L,
+                                     _P, _P, _L, _I, _I, _I, _I, _P],
     "glm52_oproj_pack": [_P, _L, _L, _I, _I, _I, _P, _P],
     "glm52_oproj_gemm": [_P, _L, _P, _L, _L, _P, _I, _P, _L, _P, _L, _I, _I, _I, _I, _P, _L,
                          _P],

@@ -15,8 +15,8 @@ the routing computed live instead of frozen, and the tail fused):
     6. shared w13 + SwiGLU      act_s[T, I]                               moe_gemm (gated, E=1)
     7. routed w2 (weighted)     Y[8T, H] = w * (act . w2^T)               moe_gemm
     8. shared w2                s[T, H]                                   moe_gemm (E=1)
-                                (weight streaming: 5+6 and 7+8 are one launch each,
-                                 moe_gemm_shared)
+                                (5+6 and 7+8 are one launch each: moe_gemm_shared when
+                                 streaming weights, moe_gemm_packed_shared at prefill)
     9. merge + ResAdd           out = bf16(sum_k Y[t, k] + h + s)         block_merge
                                 (T <= 4: 7-9 are one launch, down_token_major:
                                  out = bf16(sum_k w * (act . w2^T) + shared + h), fp32
@@ -45,7 +45,8 @@ from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
 from .kernels import add_rmsnorm as KN
 from .kernels import moe_down_merge as KD
 from .kernels import norm_router as KR
-from .kernels.moe_gateup import moe_gemm, moe_gemm_packed, moe_gemm_shared, pack_w512
+from .kernels.moe_gateup import (moe_gemm, moe_gemm_packed, moe_gemm_packed_shared,
+                                 moe_gemm_shared, pack_w512)
 
 BF16 = torch.bfloat16
 
@@ -185,8 +186,9 @@ class MoEBlock:
                                       self.align_ws)
 
     def w13_step(self):
-        """Steps 5 and 6 (at T <= 4 also 3 and 4): one launch when the shared expert runs
-        inside the routed launch, else the routed launch (the shared one is in w2_step)."""
+        """Steps 5 and 6 (at T <= 4 also 3 and 4): the routed and the shared expert in one
+        launch (weight streaming and packed prefill), else the routed launch (the shared one
+        is in w2_step)."""
         T, I, R = self.T, self.I, self.T * self.topk
         if self.front_fused:
             route_gateup_shared_into(self.logits, self.cfg_topk, self.topw, self.topi, self.sti,
@@ -196,8 +198,11 @@ class MoEBlock:
             moe_gemm_shared(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids,
                             self.ntp, R, I, I, True, self.cfg_r, self.y, self.w13s, self.act_s)
         elif self.packed:
-            moe_gemm_packed(self.y, self.topk, self.w13_p, self.act, None, self.sti, self.eids,
-                            self.ntp, R, I, True, self.cfg_r)
+            # routed and shared w13 in one launch (the shared expert's items after each
+            # XCD's routed ones)
+            moe_gemm_packed_shared(self.y, self.topk, self.w13_p, self.act, None, self.sti,
+                                   self.eids, self.ntp, R, I, True, self.cfg_r, self.y,
+                                   self.w13s_p, self.act_s)
         else:
             moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
                      R, I, I, True, self.cfg_r)
@@ -210,12 +215,9 @@ class MoEBlock:
                             self.s_out)
             return
         if self.packed:
-            moe_gemm_packed(self.y, 1, self.w13s_p, self.act_s, None, self.ssti, self.seids,
-                            self.sntp, T, I, True, self.cfg_s)
-            moe_gemm_packed(self.act, 1, self.w2_p, self.ybuf, self.topw.view(-1), self.sti,
-                            self.eids, self.ntp, R, H, False, self.cfg_r)
-            moe_gemm_packed(self.act_s, 1, self.w2s_p, self.s_out, None, self.ssti, self.seids,
-                            self.sntp, T, H, False, self.cfg_s)
+            moe_gemm_packed_shared(self.act, 1, self.w2_p, self.ybuf, self.topw.view(-1),
+                                   self.sti, self.eids, self.ntp, R, H, False, self.cfg_r,
+                                   self.act_s, self.w2s_p, self.s_out)
             return
         moe_gemm(self.y, 1, self.w13s, self.act_s, None, self.ssti, self.seids, self.sntp,
                  T, I, I, True, self.cfg_s)

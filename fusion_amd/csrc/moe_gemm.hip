@@ -523,6 +523,45 @@ extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row
   return launch_wide512(g, capacity, gated != 0, topk_weights != nullptr, stream);
 }
 
+// glm52_moe_gemm_packed with the shared expert in the same launch (prefill): an extra
+// expert with its own packed weights (glm52_pack_w512 of the [1, N, K] shared weight, same
+// n_out / k / gated) applied to rows 0 .. shared_rows - 1 of a_shared, without routing
+// weight, written to c_shared.  Its items follow each XCD's share of the routed items.
+extern "C" int glm52_moe_gemm_packed_shared(
+    const void* a, int64_t stride_am, int a_row_div, const void* w_packed, void* c,
+    int64_t stride_cm, const float* topk_weights, const int32_t* sorted_token_ids,
+    const int32_t* expert_ids, const int32_t* num_tokens_post_padded, int capacity, int block_m,
+    int num_valid_tokens, const void* a_shared, int64_t stride_as, const void* w_shared_packed,
+    void* c_shared, int64_t stride_cs, int shared_rows, int n_out, int k, int gated,
+    hipStream_t stream) {
+  if (!a || !w_packed || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded ||
+      !a_shared || !w_shared_packed || !c_shared || shared_rows < 0)
+    return GLM52_EINVAL;
+  if ((block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
+      (capacity % block_m) != 0)
+    return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 || (k % 64) != 0 ||
+      a_row_div <= 0)
+    return GLM52_EINVAL;
+  if (!al16(a) || !al16(w_packed) || (stride_am % 8) || !al16(c) || (stride_cm % 8) ||
+      !al16(a_shared) || (stride_as % 8) || !al16(w_shared_packed) || !al16(c_shared) ||
+      (stride_cs % 8))
+    return GLM52_EINVAL;
+  if (capacity == 0 && shared_rows == 0) return GLM52_OK;
+  const int ab = a_bytes(num_valid_tokens, a_row_div, stride_am, k);
+  const int axb = a_bytes(shared_rows, 1, stride_as, k);
+  if (ab < 0 || ab >= 0x7ffffff0 || axb < 0 || axb >= 0x7ffffff0) return GLM52_EUNSUPPORTED;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, a_row_div,
+             static_cast<const uint16_t*>(w_packed), 0, 0, gated ? n_out : 0,
+             static_cast<uint16_t*>(c), stride_cm, topk_weights, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
+             static_cast<const uint16_t*>(a_shared), stride_as,
+             static_cast<const uint16_t*>(w_shared_packed), static_cast<uint16_t*>(c_shared),
+             stride_cs, shared_rows, ab, axb};
+  g.Wp = static_cast<const uint16_t*>(w_packed);
+  return launch_wide512(g, capacity, gated != 0, topk_weights != nullptr, stream);
+}
+
 // The routed grouped GEMM and the shared expert's GEMM in one weight-streaming launch
 // (decode): the shared expert is an extra expert whose rows are the tokens 0 .. T - 1 of
 // its own input (no routing weight), written to its own output.  Same operand rules as

@@ -393,7 +393,13 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   const int items = num_m * num_n;
   const int nk = p.K / BKS;
   const int per_xcd = (items + 7) / 8;
-  const int span = per_xcd * 8;
+  // the extra (shared) expert, packed weights only: rows are tokens 0 .. x_rows - 1 of Ax,
+  // its row blocks' items follow each XCD's share of the routed items
+  const bool has_x = PACKED && EPI == 0 && p.Wx && p.x_rows > 0;
+  const int nbx = has_x ? (p.x_rows + MT - 1) / MT : 0;
+  const int items_x = nbx * num_n;
+  const int per_xcd_x = (items_x + 7) / 8;
+  const int span = (per_xcd + per_xcd_x) * 8;
 
   // fragment reads: lane (l32, h) reads logical chunk 2 ks + h of row base + l32 (base % 32 == 0)
   const int rd0 = l32 * BKS + (((0 + h) ^ ((l32 >> 2) & 3)) * 8);
@@ -404,37 +410,57 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   const uint32_t ring_base = lds_addr(ring);
 
   for (int it = blockIdx.x; it < span; it += gridDim.x) {
-    const int L = (it % 8) * per_xcd + it / 8;
-    if (L >= items) continue;
-    // expert-aligned order (as moe_gemm_dma_kernel): column tile major, row block fastest
-    const int b = L / num_n;
-    const int eb = p.eids[b];
-    int mb = b, me = b + 1;
-    while (mb > 0 && p.eids[mb - 1] == eb) --mb;
-    while (me < num_m && p.eids[me] == eb) ++me;
-    const int cnt = me - mb;
-    const int local = L - mb * num_n;
-    const int pid_n = local / cnt;
-    const int pid_m = mb + local % cnt;
-    const int row0 = pid_m * MT;
-    if (p.sti[row0] >= p.num_valid) continue;
-    const int e = p.eids[pid_m];
+    const int xi = it / 8 - per_xcd;  // >= 0: an item of the extra expert
+    const bool xs = xi >= 0;
+    int pid_n, row0, e;
+    if (!xs) {
+      const int L = (it % 8) * per_xcd + it / 8;
+      if (L >= items) continue;
+      // expert-aligned order (as moe_gemm_dma_kernel): column tile major, row block fastest
+      const int b = L / num_n;
+      const int eb = p.eids[b];
+      int mb = b, me = b + 1;
+      while (mb > 0 && p.eids[mb - 1] == eb) --mb;
+      while (me < num_m && p.eids[me] == eb) ++me;
+      const int cnt = me - mb;
+      const int local = L - mb * num_n;
+      pid_n = local / cnt;
+      const int pid_m = mb + local % cnt;
+      row0 = pid_m * MT;
+      if (p.sti[row0] >= p.num_valid) continue;
+      e = p.eids[pid_m];
+    } else {
+      const int Lx = (it % 8) * per_xcd_x + xi;
+      if (Lx >= items_x) continue;
+      pid_n = Lx / nbx;
+      row0 = (Lx % nbx) * MT;
+      e = 0;
+    }
     const int n0 = pid_n * NO;
     const int P = pid_n / SPLIT, sub = pid_n % SPLIT;  // the packed 512-row tile and half
+    // the item's operands: the routed rows through the layout, the extra expert's directly
+    const uint16_t* Ab = xs ? p.Ax : p.A;
+    const int64_t sam = xs ? p.sax : p.sam;
+    const int a_div = xs ? 1 : p.a_div;
+    const int nvalid = xs ? p.x_rows : p.num_valid;
+    auto tok_of = [&](int r) {  // the flat token of row r of the item (>= nvalid: padding)
+      return xs ? (row0 + r < p.x_rows ? row0 + r : p.x_rows) : p.sti[row0 + r];
+    };
 
     // real tokens fill a prefix of the block: every wave counts them (no LDS, no barrier)
     int nv_rows = 0;
 #pragma unroll
     for (int q = 0; q < MT; q += kWave)
-      nv_rows += __popcll(__ballot(q + lane < MT && p.sti[row0 + q + lane] < p.num_valid));
+      nv_rows += __popcll(__ballot(q + lane < MT && tok_of(q + lane) < nvalid));
     nv_rows = __builtin_amdgcn_readfirstlane(nv_rows);
     const int nvf = __builtin_amdgcn_readfirstlane(max(0, min(TF, (nv_rows - wm * TPW + 31) / 32)));
 
     // W load instruction i of the wave fills slab rows (wv * WI + i) * 16 .. +15 of the
     // tile: packed, 1 KB of contiguous memory; in place, W rows wrow + phi32(lane / 4), 16
     // bytes at logical chunk dc each (the lane's byte offsets inside W[e], < 2^32)
-    const uint16_t* wexp = PACKED ? p.Wp + ((int64_t)(e * num_n512 + P) * nk * SPLIT + sub) *
-                                               (kPackStage / 2 / SPLIT)
+    const uint16_t* wexp = PACKED ? (xs ? p.Wx : p.Wp) +
+                                        ((int64_t)(e * num_n512 + P) * nk * SPLIT + sub) *
+                                            (kPackStage / 2 / SPLIT)
                                   : p.W + (int64_t)e * p.swe;
     uint32_t wvoff[WI];
 #pragma unroll
@@ -451,7 +477,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       const int rl = wv * (MT / 4) + i * RPI + dr;
-      avoff[i] = (uint32_t)((p.sti[row0 + (rl < nv_rows ? rl : 0)] / p.a_div) * (int)p.sam + dc * 8) * 2u;
+      avoff[i] = (uint32_t)((tok_of(rl < nv_rows ? rl : 0) / a_div) * (int)sam + dc * 8) * 2u;
     }
 
     // the previous item's output stores and loads are done before this item's are counted
@@ -464,7 +490,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
         dma16s(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
       } else {
         const int j = i - WI;
-        dma16s(p.A + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
+        dma16s(Ab + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
       }
     };
 
@@ -558,9 +584,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 
 #pragma unroll
       for (int t = 0; t < NV; ++t) {
-        const int tok = p.sti[row0 + wm * TPW + t * 32 + l32];
-        if (tok >= p.num_valid) continue;
-        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;  // EPI 0, 1
+        const int tok = tok_of(wm * TPW + t * 32 + l32);
+        if (tok >= nvalid) continue;
+        uint16_t* crow = EPI >= 2 ? nullptr
+                                  : (xs ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm);
         if (GATED) {
 #pragma unroll
           for (int fp = 0; fp < 2; ++fp) {
@@ -573,7 +600,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
           }
         } else {
           float wgt = 1.f;
-          if (WEIGHTED) wgt = p.topw[tok];
+          if (WEIGHTED && !xs) wgt = p.topw[tok];
 #pragma unroll
           for (int f = 0; f < 4; ++f) {
             float v[16];
@@ -633,7 +660,8 @@ template <int MT, int NTW, bool GATED, bool WEIGHTED>
 int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
   constexpr int NO = GATED ? NTW / 2 : NTW;
   if ((a.n_out % (GATED ? 256 : 512)) || (a.K % 64)) return GLM52_EUNSUPPORTED;
-  const int items_max = (capacity / MT) * (a.n_out / NO);
+  const int x_blocks = (a.Wp && a.Wx && a.x_rows > 0) ? (a.x_rows + MT - 1) / MT : 0;
+  const int items_max = (capacity / MT + x_blocks) * (a.n_out / NO);
   int grid = items_max < 256 ? items_max : 256;
   grid = ((grid + 7) / 8) * 8;
   if constexpr (!GATED && !WEIGHTED) {

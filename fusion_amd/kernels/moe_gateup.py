@@ -131,6 +131,41 @@ def moe_gemm_packed(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids, e
     )
 
 
+def moe_gemm_packed_shared(a, a_row_div, w_packed, c, topk_weights, sorted_token_ids,
+                           expert_ids, num_tokens_post_padded, num_valid_tokens, n_out, gated,
+                           cfg, a_shared, w_shared_packed, c_shared):
+    """`moe_gemm_packed` with the shared expert in the same launch: `w_shared_packed`
+    (`pack_w512` of the [1, N, K] shared weight) applied to every row of `a_shared` (one
+    row per token, no routing weight), written to `c_shared`."""
+    _lib.require_gpu(a, w_packed, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
+                     topk_weights, a_shared, w_shared_packed, c_shared)
+    for t, n in ((a, "a"), (w_packed, "w_packed"), (c, "c"), (a_shared, "a_shared"),
+                 (w_shared_packed, "w_shared_packed"), (c_shared, "c_shared")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be bf16 and contiguous along its last dim")
+    if topk_weights is not None and (topk_weights.dtype != torch.float32
+                                     or not topk_weights.is_contiguous()):
+        raise ValueError("topk weights must be a contiguous fp32 tensor")
+    if a_shared.shape[1] != a.shape[1] or c_shared.shape[0] != a_shared.shape[0]:
+        raise ValueError("a_shared / c_shared rows must match (one per token)")
+    check_packed(w_packed, n_out, a.shape[1], gated)
+    check_packed(w_shared_packed, n_out, a.shape[1], gated)
+    if getattr(w_shared_packed, "glm52_pack", (1,))[0] != 1:
+        raise ValueError("w_shared_packed must hold one expert")
+    bm = int(cfg["BLOCK_M"])
+    cap = check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, bm)
+    if num_valid_tokens == 0 and a_shared.shape[0] == 0:
+        return
+    _lib.call(
+        "glm52_moe_gemm_packed_shared", _lib.ptr(a), a.stride(0), int(a_row_div),
+        _lib.ptr(w_packed), _lib.ptr(c), c.stride(0), _lib.ptr(topk_weights),
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded), cap,
+        bm, int(num_valid_tokens), _lib.ptr(a_shared), a_shared.stride(0),
+        _lib.ptr(w_shared_packed), _lib.ptr(c_shared), c_shared.stride(0), a_shared.shape[0],
+        int(n_out), a.shape[1], int(gated), _lib.stream(),
+    )
+
+
 def moe_gemm_shared(a, a_row_div, w, c, topk_weights, sorted_token_ids, expert_ids,
                     num_tokens_post_padded, num_valid_tokens, n_out, gate_up_offset, gated, cfg,
                     a_shared, w_shared, c_shared):

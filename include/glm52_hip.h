@@ -215,6 +215,22 @@ int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row_div, const
                           const int32_t* num_tokens_post_padded, int capacity, int block_m,
                           int num_valid_tokens, int n_out, int k, int gated, hipStream_t stream);
 
+/* glm52_moe_gemm_packed with the shared expert in the same launch (prefill, block_m 64,
+ * 128 or 256): an extra expert whose packed weights w_shared_packed (glm52_pack_w512 of
+ * the [1, N, K] shared weight, same n_out / k / gated) apply to rows 0 .. shared_rows - 1
+ * of a_shared, without routing weight, written to c_shared.  Replaces the routed + shared
+ * launch pairs of the reference chain (launch_gateup twice, launch_down twice:
+ * glm52/bench/bench_layer.py:430-480) for block sizes 64 and up. */
+int glm52_moe_gemm_packed_shared(const void* a, int64_t stride_am, int a_row_div,
+                                 const void* w_packed, void* c, int64_t stride_cm,
+                                 const float* topk_weights, const int32_t* sorted_token_ids,
+                                 const int32_t* expert_ids,
+                                 const int32_t* num_tokens_post_padded, int capacity,
+                                 int block_m, int num_valid_tokens, const void* a_shared,
+                                 int64_t stride_as, const void* w_shared_packed, void* c_shared,
+                                 int64_t stride_cs, int shared_rows, int n_out, int k, int gated,
+                                 hipStream_t stream);
+
 /* o_proj + ResAdd1, the dense GEMM upstream of the block (`glm52/kernels/oproj_resadd.py`).
  * A [M, K] bf16 (K contiguous), B [K, N] bf16 (strides in elements), r [M, N] bf16.
  *   glm52_oproj_gemm: c = A @ B with the epilogue of oproj_gemm_kernel: r non-null adds
