@@ -14,7 +14,7 @@
 //
 // Every kernel walks (row, 8-column chunk) pairs with a grid-stride loop and moves each
 // byte with one 128-bit access; all top-k loads of a chunk are issued before any add.
-#include "common.h"
+#include "moe_gemm.h"
 
 using namespace glm52;
 
@@ -172,10 +172,12 @@ __global__ __launch_bounds__(kBlock) void block_merge_kernel(
     const int c = (int)(q % cpr);
     uint4 v[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const uint4*>(y + t * syt + k * syk + c * 8);
-    const uint4 hv = *reinterpret_cast<const uint4*>(h + t * sh + c * 8);
+    // every input is read once and the output is not read again in the block: all
+    // non-temporal (T = 8192, 1.1 GB moved: 257 -> 195 us after the benchmark's flush)
+    for (int k = 0; k < 8; ++k) v[k] = ldg_nt(y + t * syt + k * syk + c * 8);
+    const uint4 hv = ldg_nt(h + t * sh + c * 8);
     uint4 sv = make_uint4(0, 0, 0, 0);
-    if (HAS_SHARED) sv = *reinterpret_cast<const uint4*>(s + t * ss + c * 8);
+    if (HAS_SHARED) sv = ldg_nt(s + t * ss + c * 8);
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -193,7 +195,7 @@ __global__ __launch_bounds__(kBlock) void block_merge_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] += f[j];
     }
-    *reinterpret_cast<uint4*>(out + t * so + c * 8) = pack8(acc);
+    stg_nt(out + t * so + c * 8, pack8(acc));
   }
 }
 
@@ -304,7 +306,6 @@ extern "C" int glm52_block_merge(const void* y, int64_t stride_yt, int64_t strid
 // equals a magic value (never, for a real buffer), which keeps the loads alive.
 // ------------------------------------------------------------------------------------
 namespace {
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 template <bool NT>
 __global__ __launch_bounds__(kBlock) void stream_read_kernel(const uint4* __restrict__ p,

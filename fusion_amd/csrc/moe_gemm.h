@@ -30,6 +30,12 @@ GLM52_DEV uint4 ldg_nt(const uint16_t* p) {
 
 GLM52_DEV uint4 ldg(const uint16_t* p) { return *reinterpret_cast<const uint4*>(p); }
 
+// 16-byte store with the non-temporal hint: for outputs no kernel of this launch reads.
+GLM52_DEV void stg_nt(uint16_t* p, const uint4& v) {
+  u32x4_t w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4_t*>(p));
+}
+
 // Raw buffer resource over `bytes` bytes at `base` (gfx9 descriptor word 3 for raw,
 // range-checked 32-bit loads): a load whose offset is out of range returns zero without
 // touching memory.
