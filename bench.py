@@ -58,6 +58,9 @@ def parse():
     ap.add_argument("--pmc-child", action="store_true",
                     help="(internal) the process profiled for roofline.traffic: three 256 MiB "
                          "copies, then the block's w13 launch at the first --tokens value")
+    ap.add_argument("--pmc-step", default="w13", choices=("w13", "w2", "block"),
+                    help="(with --pmc-child) the launch profiled: the block's w13 launch, its "
+                         "w2 launch, or the whole block")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run a plain 256 MiB device copy three times: the known-size "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -107,11 +110,12 @@ def main() -> int:
                        W.w13s, W.w2s)
         blk(x, r)
         torch.cuda.synchronize()
+        step = {"w13": blk.w13_step, "w2": blk.w2_step, "block": lambda: blk(x, r)}[args.pmc_step]
         for _ in range(PMC_LAUNCHES):
             flush_buf.zero_()
-            blk.w13_step()
+            step()
         torch.cuda.synchronize()
-        log(f"pmc child: T={T}, {PMC_LAUNCHES} w13 launches")
+        log(f"pmc child: T={T}, {PMC_LAUNCHES} {args.pmc_step} launches")
         return 0
 
     def flush():
