@@ -7,24 +7,30 @@
 // Evaluating every logit that way costs an fp64 GEMM.  Here:
 //
 // 1. router_approx_kernel: L~[t, e] on `v_mfma_f32_32x32x16_bf16`.  The products are exact
-//    in fp32; each accumulator runs a chain of eight MFMAs (128 k) and is then added into
-//    an fp64 sum.  An MFMA adds 16 products to its accumulator with at most 16 roundings
-//    of a partial sum no larger than |acc| + its |products|, so a chain of eight errs by
-//    at most 16 * 9 * 2^-23 times the chain's sum of |products|, and |L~ - sum| <=
-//    1.125 * 2^-16 * sum_k |y_k w_k| over the
-//    row, and sum_k |y_k w_k| <= ||y|| ||w_e|| (Cauchy-Schwarz).  The kernel also returns
-//    the sums of squares of every gate row (those of y come from the token's row in 2.).  A workgroup owns 64 tokens x all
-//    experts of one K slice (K is split until about 256 workgroups run; fp32 partials).
+//    in fp32; each accumulator runs a chain of eight MFMAs (128 k), and the chains of a K
+//    slice are summed in fp32.  An MFMA adds 16 products to its accumulator with at most 16
+//    roundings of a partial sum no larger than |acc| + its |products|, so a chain of eight
+//    errs by at most 16 * 9 * 2^-23 = 1.125 * 2^-16 times the chain's sum of |products|;
+//    each of the m <= H / 128 additions of a chain into the slice sum errs by at most
+//    2^-24 times the slice's sum of |products| (m * 2^-24 <= 0.25 * 2^-16 at H = 8192).
+//    The slices' fp32 sums are added in fp64 and rounded once, so |L~ - sum| <=
+//    1.375 * 2^-16 * sum_k |y_k w_k| + 2^-24 |L~|, and sum_k |y_k w_k| <= ||y|| ||w_e||
+//    (Cauchy-Schwarz).  The kernel also returns the sums of squares of the token rows and
+//    of the gate rows over each slice.  A workgroup owns 64 tokens (128 from 4096 tokens)
+//    x all experts of one K slice (K is split until about 256 workgroups run; fp32
+//    partials), its eight waves reading 2 x 2 (2 x 1) blocks of 32 x 32 from a three-stage
+//    LDS ring of 64-k stages (one 128-byte segment per row and stage).
 // 2. router_select_kernel, one wave per token: from L~ and the bound
-//    B = 2.5 * 2^-16 * ||y|| ||w_e|| + 2^-21 |L~| (over twice the chain bound, plus the fp32
-//    roundings of L~ and of the exact logit), each expert's exact key lies in
+//    B = 2.5 * 2^-16 * ||y|| ||w_e|| + 2^-21 |L~| (above the bound of 1. plus the fp32
+//    rounding of the exact logit), each expert's exact key lies in
 //    [lo, hi] = [sig(L~ - B) + b - d, sig(L~ + B) + b + d] (d covers the fp32 roundings
 //    and the fast sigmoid).  Every expert of the exact top k has key >= the k-th largest
 //    lo, so the candidates {e : hi_e >= that} hold the whole top k, and no other expert
 //    can tie with its k-th key.  Only the candidates (about k per token) get the exact
-//    logit -- an fp64 dot product of y and the gate row -- and the exact top k is taken
-//    among them: the same ids, order and weights as the exact rule over all experts.
-//    Non-finite values make every expert a candidate.
+//    logit -- an fp64 dot product of y and the gate row, eight (then four) rows per pass
+//    over the token row -- and the exact top k is taken among them by rank: the same ids,
+//    order and weights as the exact rule over all experts.  Non-finite values make every
+//    expert a candidate.
 //
 // The logits written are exact for the candidates (so for every selected expert) and
 // L~ rounded to fp32 elsewhere (within B of the exact logit).
@@ -35,12 +41,15 @@ using namespace glm52;
 
 namespace {
 
-constexpr int kTok = 64;                 // tokens per workgroup of the approximate pass
-constexpr int kBk = 32;                  // k per LDS stage
-constexpr int kStages = 7;               // LDS ring
-constexpr int kRows = kMaxE + kTok;      // gate rows (E padded to 256) + token rows
-constexpr int kStageElems = kRows * kBk; // 20 KB per stage
-constexpr int kIps = 5;                  // loads per wave and stage: 4 gate + 1 token
+constexpr int kBk = 64;                  // k per LDS stage (one 128-byte segment of a row)
+constexpr int kStages = 3;               // LDS ring
+constexpr int kWaves = 8;                // waves per workgroup of the approximate pass
+constexpr int kGateIps = kMaxE / (8 * kWaves);  // loads per wave and stage: 8 rows each
+
+// tokens per workgroup of the approximate pass: 128 from 4096 tokens, else 64 (more
+// workgroups for the smaller batches)
+constexpr int kBigTokT = 4096;
+inline int approx_tok(int T) { return T >= kBigTokT ? 128 : 64; }
 constexpr int kMaxH = 8192;
 
 GLM52_DEV float sumsq8(const uint4& v) {
@@ -52,61 +61,89 @@ GLM52_DEV float sumsq8(const uint4& v) {
   return s;
 }
 
-// grid = (ceil(T / 64), KS); block = 256.  Wave w computes expert blocks 2w, 2w + 1 (of
-// 32) against both 32-token blocks.  out: KS == 1: L~ into logits [T, E] (row stride
-// so); else fp32 partials part[ks][T][E].  ssw[ks][E]: the gate rows' sums of squares
-// over slice ks.
-__global__ __launch_bounds__(256) void router_approx_kernel(
+// grid = ceil(T / 128) * KS; block = 512.  Wave w computes expert blocks 2 (w % 4) + f
+// (of 32) against token blocks 2 (w / 4) + j, f, j in {0, 1}.  out: KS == 1: L~ into logits [T, E] (row stride
+// so); else fp32 partials part[ks][T][E].  ssw[ks][E] / ssy[ks][T]: the gate rows' / the
+// token rows' sums of squares over slice ks (fp32, one chain of at most H / 2 fused
+// multiply-adds per lane: within 2^-11 relative of the exact sums).
+template <int TOK>
+__global__ __launch_bounds__(512) void router_approx_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const uint16_t* __restrict__ gate, int64_t sg,
-    int T, int H, int E, float* __restrict__ out, int64_t so, float* __restrict__ ssw) {
+    int T, int H, int E, int KS, float* __restrict__ out, int64_t so, float* __restrict__ ssw,
+    float* __restrict__ ssy) {
+  constexpr int kTok = TOK;
+  constexpr int TB = TOK / 64;                      // token blocks per wave
+  constexpr int kStageElems = (kMaxE + kTok) * kBk; // gate rows (E padded to 256) + token rows
+  constexpr int kTokIps = kTok / (8 * kWaves);      // token-row loads per wave and stage
+  constexpr int kIps = kGateIps + kTokIps;
   __shared__ __attribute__((aligned(1024))) uint16_t ring[kStages * kStageElems];
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
   const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int l32 = lane % 32, h = lane / 32;
-  const int t0 = blockIdx.x * kTok;
-  const int ks = blockIdx.y, KS = gridDim.y;
+  // the workgroups of one K slice run on the same XCDs (hardware workgroup h runs on XCD
+  // h % 8), so the slice's gate rows are shared through those XCDs' L2: logical index L,
+  // slice L / nb, token block L % nb
+  const int nb = (T + kTok - 1) / kTok;
+  const int nwg = nb * KS;
+  const int xcd = blockIdx.x % 8, q8 = nwg / 8, r8 = nwg % 8;
+  const int L = (xcd < r8 ? xcd * (q8 + 1) : r8 * (q8 + 1) + (xcd - r8) * q8) + blockIdx.x / 8;
+  const int ks = L / nb, tb = L % nb;
+  const int t0 = tb * kTok;
   const int ksl = H / KS;
   const int kbeg = ks * ksl;
   const int nk = ksl / kBk;
 
-  // load slots: lane -> row lane / 4 of a 16-row slab, physical chunk lane % 4 holding
-  // logical chunk dc (the read side applies the same swizzle)
-  const int dr = lane >> 2;
-  const int dc = (lane & 3) ^ ((dr >> 2) & 3);
-  uint32_t goff[4];
+  // load slots: lane -> row lane / 8 of an 8-row slab (a 128-byte segment per row),
+  // physical 16-byte chunk lane % 8 holding logical chunk (lane % 8) ^ ((row / 2) % 8): the
+  // MFMA operand reads of 16 consecutive rows then hit 16 different bank groups
+  const int dr = lane >> 3;
+  auto chunk_of = [&](int slab) { return (lane & 7) ^ ((((slab & 1) << 2) + (dr >> 1)) & 7); };
+  uint32_t goff[kGateIps];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int er = min((wv * 4 + i) * 16 + dr, E - 1);  // padded experts re-read a real row
-    goff[i] = (uint32_t)((er * sg + dc * 8) * 2);
+  for (int i = 0; i < kGateIps; ++i) {
+    const int slab = wv * kGateIps + i;
+    const int er = min(slab * 8 + dr, E - 1);  // padded experts re-read a real row
+    goff[i] = (uint32_t)((er * sg + chunk_of(slab) * 8) * 2);
   }
-  const int yrow = wv * 16 + dr;
   const uint16_t* ybase = y + (int64_t)t0 * sy;
-  const uint32_t yoff = (uint32_t)((min(yrow, T - 1 - t0) * sy + dc * 8) * 2);
+  uint32_t yoff[kTokIps];
+#pragma unroll
+  for (int i = 0; i < kTokIps; ++i) {
+    const int slab = wv * kTokIps + i;  // kMaxE / 8 is even: same parity as its ring row
+    yoff[i] = (uint32_t)((min(slab * 8 + dr, T - 1 - t0) * sy + chunk_of(slab) * 8) * 2);
+  }
   const uint32_t ring_base = lds_addr(ring);
 
   auto issue = [&](int s) {
     const int kc = kbeg + min(s, nk - 1) * kBk;
     const uint32_t sb = ring_base + (uint32_t)((s % kStages) * kStageElems * 2);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16s(gate + kc, goff[i], sb + (uint32_t)((wv * 4 + i) * 16 * kBk * 2));
-    dma16s(ybase + kc, yoff, sb + (uint32_t)((kMaxE + wv * 16) * kBk * 2));
+    for (int i = 0; i < kGateIps; ++i)
+      dma16s(gate + kc, goff[i], sb + (uint32_t)((wv * kGateIps + i) * 8 * kBk * 2));
+#pragma unroll
+    for (int i = 0; i < kTokIps; ++i)
+      dma16s(ybase + kc, yoff[i], sb + (uint32_t)((kMaxE + (wv * kTokIps + i) * 8) * kBk * 2));
   };
 
-  const int rd0 = l32 * kBk + (((0 + h) ^ ((l32 >> 2) & 3)) * 8);
-  const int rd1 = l32 * kBk + (((2 + h) ^ ((l32 >> 2) & 3)) * 8);
-
-  floatx16_t acc[2][2];   // [expert block][token block]
-  double dacc[2][2][16];
+  const int eb0 = (wv % 4) * 2, tb0 = (wv / 4) * TB;
+  floatx16_t acc[2][TB];   // [expert block][token block]: chains of at most eight MFMAs
+  floatx16_t acc2[2][TB];  // the chains' sum
 #pragma unroll
   for (int f = 0; f < 2; ++f)
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
+    for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         acc[f][tb][i] = 0.f;
-        dacc[f][tb][i] = 0.0;
+        acc2[f][tb][i] = 0.f;
       }
+  float ysq = 0.f;  // waves w % 4 < TB: the sum of squares of token block tb0 + w % 4's row l32 (half h)
+  // the gate rows' sums of squares over the slice: with at least 8 token blocks, workgroup
+  // tb < 8 takes expert block tb from the operands of wave tb / 2 (f = tb % 2); else a
+  // loop over global memory after the main loop
+  const bool gsq_on = nb >= 8 && tb < 8 && wv == tb / 2;
+  float gsq = 0.f;
 #pragma unroll
   for (int s = 0; s < kStages - 1; ++s) issue(s);
 #pragma unroll 1
@@ -116,37 +153,58 @@ __global__ __launch_bounds__(256) void router_approx_kernel(
     issue(s + kStages - 1);
     const uint16_t* sb = ring + (s % kStages) * kStageElems;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int rd = kk ? rd1 : rd0;
-      uint4 a[2], b[2];
+    for (int kk = 0; kk < kBk / 16; ++kk) {
+      const int rd = l32 * kBk + (((2 * kk + h) ^ ((l32 >> 1) & 7)) * 8);
+      uint4 a[2], b[TB];
 #pragma unroll
       for (int f = 0; f < 2; ++f)
-        a[f] = *reinterpret_cast<const uint4*>(sb + ((wv * 2 + f) * 32) * kBk + rd);
+        a[f] = *reinterpret_cast<const uint4*>(sb + ((eb0 + f) * 32) * kBk + rd);
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb)
-        b[tb] = *reinterpret_cast<const uint4*>(sb + (kMaxE + tb * 32) * kBk + rd);
+      for (int tb = 0; tb < TB; ++tb)
+        b[tb] = *reinterpret_cast<const uint4*>(sb + (kMaxE + (tb0 + tb) * 32) * kBk + rd);
 #pragma unroll
       for (int f = 0; f < 2; ++f)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) acc[f][tb] = mfma32(a[f], b[tb], acc[f][tb]);
+        for (int tb = 0; tb < TB; ++tb) acc[f][tb] = mfma32(a[f], b[tb], acc[f][tb]);
+      // both sums, then a select of the result: a runtime choice between array elements
+      // becomes a dynamically indexed private array (LDS or scratch), and a scratch load
+      // inside this loop would wait for the ring's loads
+      if (wv % 4 < TB) {
+        const float q0 = sumsq8(b[0]), q1 = TB == 2 ? sumsq8(b[TB - 1]) : 0.f;
+        ysq += (TB == 2 && wv % 4 == 1) ? q1 : q0;
+      }
+      if (gsq_on) {
+        const float q0 = sumsq8(a[0]), q1 = sumsq8(a[1]);
+        gsq += (tb & 1) ? q1 : q0;
+      }
     }
-    if ((s & 3) == 3 || s == nk - 1) {  // chains of at most eight MFMAs, then into fp64
+    if ((s & 1) == 1 || s == nk - 1) {  // chains of at most eight MFMAs, then into the sum
 #pragma unroll
       for (int f = 0; f < 2; ++f)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
+        for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            dacc[f][tb][i] += (double)acc[f][tb][i];
+            acc2[f][tb][i] += acc[f][tb][i];
             acc[f][tb][i] = 0.f;
           }
     }
   }
   GLM52_WAIT_VMCNT(0);  // the clamped loads past the slice
+  if (wv % 4 < TB) {
+    ysq += __shfl_xor(ysq, 32, kWave);
+    const int t = t0 + (tb0 + wv % 4) * 32 + l32;
+    if (h == 0 && t < T) ssy[(int64_t)ks * T + t] = ysq;
+  }
 
-  // sums of squares of the gate rows over this K slice: row e by workgroup e % nblocks,
-  // a wave per row, from global memory (the rows were just streamed: L2 hits)
-  for (int e = blockIdx.x + wv * gridDim.x; e < E; e += 4 * gridDim.x) {
+  if (gsq_on) {
+    gsq += __shfl_xor(gsq, 32, kWave);
+    const int e = tb * 32 + l32;
+    if (h == 0 && e < E) ssw[(int64_t)ks * E + e] = gsq;
+  }
+  // fewer than 8 token blocks: row e by workgroup e % nb, a wave per row, from global
+  // memory (the rows were just streamed: L2 hits)
+  for (int e = tb + wv * nb; nb < 8 && e < E; e += kWaves * nb) {
     const uint16_t* grow = gate + (int64_t)e * sg + kbeg;
     float q = 0.f;
     for (int c = lane; c < ksl / 8; c += kWave) q += sumsq8(*reinterpret_cast<const uint4*>(grow + c * 8));
@@ -154,19 +212,29 @@ __global__ __launch_bounds__(256) void router_approx_kernel(
     if (lane == 0) ssw[(int64_t)ks * E + e] = q;
   }
 
-  // result i of lane (l32, h) in block (f, tb): expert (2 wv + f) * 32 + 8 (i / 4) + 4 h +
-  // i % 4, token t0 + 32 tb + l32
+  // result i of lane (l32, h) in block (f, tb): expert (eb0 + f) * 32 + 8 (i / 4) + 4 h +
+  // i % 4, token t0 + 32 (tb0 + tb) + l32
 #pragma unroll
-  for (int tb = 0; tb < 2; ++tb) {
-    const int t = t0 + tb * 32 + l32;
+  for (int tb = 0; tb < TB; ++tb) {
+    const int t = t0 + (tb0 + tb) * 32 + l32;
     if (t < T) {
       float* orow = KS == 1 ? out + (int64_t)t * so : out + ((int64_t)ks * T + t) * E;
+      const bool al16 = (reinterpret_cast<uintptr_t>(orow) & 15u) == 0;
 #pragma unroll
       for (int f = 0; f < 2; ++f)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int e = (wv * 2 + f) * 32 + 8 * (i / 4) + 4 * h + (i % 4);
-          if (e < E) orow[e] = (float)dacc[f][tb][i];
+        for (int q = 0; q < 4; ++q) {
+          const int e = (eb0 + f) * 32 + 8 * q + 4 * h;  // E % 4 == 0: e < E covers e + 3
+          if (e < E) {
+            if (al16) {
+              *reinterpret_cast<float4*>(orow + e) =
+                  make_float4(acc2[f][tb][4 * q], acc2[f][tb][4 * q + 1], acc2[f][tb][4 * q + 2],
+                              acc2[f][tb][4 * q + 3]);
+            } else {
+#pragma unroll
+              for (int u = 0; u < 4; ++u) orow[e + u] = acc2[f][tb][4 * q + u];
+            }
+          }
         }
     }
   }
@@ -215,74 +283,78 @@ GLM52_DEV double wave_sum_f64_dpp(double v) {
   return ((row(0) + row(16)) + row(32)) + row(48);
 }
 
-// fp64 dot products of the token row (held as yr) with two gate rows, each as four
-// interleaved partial sums (any order of exact products rounds to the same fp32)
-template <int NQ>
-GLM52_DEV void dot2_f64(const uint4 (&yr)[NQ], const uint16_t* g0, const uint16_t* g1,
-                        double* out0, double* out1) {
+// Exact logits of G candidate experts of one token, by one wave: fp64 dot products of
+// the token row and the gate rows ids[0, G) (an LDS list), lane l holding the 16-byte
+// chunks l + 64 q of every row, one fp64 accumulator per row (any order of the exact
+// products rounds to the same fp32).  One K step loads the token chunk and the G gate
+// chunks, then converts the token chunk once for all G rows.  Results are wave-uniform.
+template <int NQ, int G>
+GLM52_DEV void dots_f64(const uint16_t* __restrict__ yrow, const uint16_t* __restrict__ gate,
+                        int64_t sg, const int* ids, double (&out)[G]) {
   const int lane = threadIdx.x % kWave;
-  uint4 a[NQ], b[NQ];
+  const uint16_t* g[G];
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {  // every load in flight before the first product
-    a[q] = *reinterpret_cast<const uint4*>(g0 + (lane + kWave * q) * 8);
-    b[q] = *reinterpret_cast<const uint4*>(g1 + (lane + kWave * q) * 8);
-  }
-  double s0[4] = {0.0, 0.0, 0.0, 0.0}, s1[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int c = 0; c < G; ++c) g[c] = gate + (int64_t)__builtin_amdgcn_readfirstlane(ids[c]) * sg;
+  double acc[G];
 #pragma unroll
+  for (int c = 0; c < G; ++c) acc[c] = 0.0;
+#pragma unroll 2
   for (int q = 0; q < NQ; ++q) {
-    float yf[8], af[8], bf[8];
-    unpack8(yr[q], yf);
-    unpack8(a[q], af);
-    unpack8(b[q], bf);
+    const int off = (lane + kWave * q) * 8;
+    const uint4 yv = *reinterpret_cast<const uint4*>(yrow + off);
+    uint4 gv[G];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      s0[i % 4] = fma((double)yf[i], (double)af[i], s0[i % 4]);
-      s1[i % 4] = fma((double)yf[i], (double)bf[i], s1[i % 4]);
+    for (int c = 0; c < G; ++c) gv[c] = *reinterpret_cast<const uint4*>(g[c] + off);
+    float yf[8];
+    unpack8(yv, yf);
+    double yd[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) yd[i] = (double)yf[i];
+#pragma unroll
+    for (int c = 0; c < G; ++c) {
+      float gf[8];
+      unpack8(gv[c], gf);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[c] = fma(yd[i], (double)gf[i], acc[c]);
     }
   }
-  *out0 = wave_sum_f64_dpp((s0[0] + s0[1]) + (s0[2] + s0[3]));
-  *out1 = wave_sum_f64_dpp((s1[0] + s1[1]) + (s1[2] + s1[3]));
+#pragma unroll
+  for (int c = 0; c < G; ++c) out[c] = wave_sum_f64_dpp(acc[c]);
 }
 
 // One wave per token, four tokens per workgroup; H = NQ * 512.  part: the KS fp32
-// partials, or null when KS == 1 (the logits array then holds L~).
+// partials, or null when KS == 1 (the logits array then holds L~).  ssy[ks][t] / ssw[ks][e]:
+// the token rows' / gate rows' sums of squares over slice ks (from router_approx_kernel).
 template <int NQ>
 __global__ __launch_bounds__(256) void router_select_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const uint16_t* __restrict__ gate, int64_t sg,
     const float* __restrict__ part, int KS, const float* __restrict__ ssw,
-    const float* __restrict__ bias, float* __restrict__ logits,
+    const float* __restrict__ ssy, const float* __restrict__ bias, float* __restrict__ logits,
     int64_t sl, float* __restrict__ topw, int64_t stw, int32_t* __restrict__ topi, int64_t sti,
     int T, int E, int topk, float scale, int norm_prob) {
   __shared__ float sel_s[4][8];
   __shared__ int sel_i[4][8];
   __shared__ int cand[4][kMaxE];
+  __shared__ float clg[4][kMaxE];          // the candidates' exact logits (fp32)
+  __shared__ uint64_t cord[4][kMaxE];      // (key order, 0xffff - expert): larger ranks first
   const int lane = threadIdx.x % kWave;
   const int wv = threadIdx.x / kWave;
   const int64_t t = (int64_t)blockIdx.x * 4 + wv;
   const bool t_ok = t < T;  // wave-uniform
 
-  // the token's y row, 16-byte chunk lane + 64 q per lane
-  uint4 yr[NQ];
-#pragma unroll
-  for (int q = 0; q < NQ; ++q)
-    yr[q] = t_ok ? *reinterpret_cast<const uint4*>(y + t * sy + (lane + kWave * q) * 8)
-                 : make_uint4(0, 0, 0, 0);
-
   float bv[4];
   load_bias(bias, E, bv);
-  float sy2 = 0.f;  // the row's sum of squares, from the registers
-#pragma unroll
-  for (int q = 0; q < NQ; ++q) sy2 += sumsq8(yr[q]);
-  sy2 = wave_sum(sy2) * (1.0f + 0x1p-10f);  // an upper bound of the exact sum
 
-  // L~ and the gate-row sums of squares of the lane's experts, the K slices' values
-  // loaded eight at a time (all in flight) and summed in slice order
+  // L~, the gate rows' sums of squares of the lane's experts and the token row's sum of
+  // squares: the K slices' values loaded eight at a time (all in flight), summed in order
   double la[4] = {0.0, 0.0, 0.0, 0.0};
   float sw[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int k0 = 0; k0 < KS; k0 += 8) {
-    float pv[8][4], wv8[8][4];
+  float sy2 = 0.f;
+  for (int k0 = 0; k0 < KS; k0 += 4) {
+    float pv[4][4], wv8[4][4], yv8[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i) {
+      yv8[i] = t_ok && k0 + i < KS ? ssy[(int64_t)(k0 + i) * T + t] : 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int e = lane + j * kWave;
@@ -290,22 +362,23 @@ __global__ __launch_bounds__(256) void router_select_kernel(
         pv[i][j] = ok ? (part ? part[((int64_t)(k0 + i) * T + t) * E + e] : logits[t * sl + e]) : 0.f;
         wv8[i][j] = ok ? ssw[(int64_t)(k0 + i) * E + e] : 0.f;
       }
+    }
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 4; ++i) {
+      sy2 += yv8[i];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         la[j] += (double)pv[i][j];
         sw[j] += wv8[i][j];
       }
+    }
   }
+  sy2 *= 1.0f + 0x1p-10f;  // an upper bound of the exact sum
 
-  float sc[4], key[4];
   uint32_t ol[4], oh[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int e = lane + j * kWave;
-    sc[j] = 0.f;
-    key[j] = -INFINITY;
     ol[j] = 0u;
     oh[j] = 0u;
     if (t_ok && e < E) {
@@ -352,46 +425,68 @@ __global__ __launch_bounds__(256) void router_select_kernel(
   }
 
   // the candidates, listed in expert order
-  uint32_t absent = 0u;
   int nc = 0;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const bool c = t_ok && lane + j * kWave < E && oh[j] >= kth;
-    if (!c) absent |= 1u << j;
     const uint64_t m = __ballot(c);
     if (c) cand[wv][nc + __popcll(m & ((1ull << lane) - 1ull))] = lane + j * kWave;
     nc += __popcll(m);
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): the list is written (one wave)
 
-  // exact logits of the candidates, two at a time; the owner lane of each takes its score
-  // and key
-  for (int i = 0; i < nc; i += 2) {
-    const int e0 = cand[wv][i];
-    const int e1 = i + 1 < nc ? cand[wv][i + 1] : e0;
-    double d0, d1;
-    dot2_f64<NQ>(yr, gate + (int64_t)e0 * sg, gate + (int64_t)e1 * sg, &d0, &d1);
+  // exact logits of the candidates, eight at a time, then four at a time (the last group
+  // repeats its first row where the list runs out)
+  const uint16_t* yrow = y + t * sy;
+  int i = 0;
+  for (; i + 8 <= nc; i += 8) {
+    double d[8];
+    dots_f64<NQ, 8>(yrow, gate, sg, &cand[wv][i], d);
+    if (lane < 8) {
+      double v = d[0];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int e = u ? e1 : e0;
-      const float lx = (float)(u ? d1 : d0);
-      const float s = (float)(1.0 / (1.0 + exp(-(double)lx)));
-      if (lane == e % kWave) {
-        const int j = e / kWave;
-        const float b = j == 0 ? bv[0] : j == 1 ? bv[1] : j == 2 ? bv[2] : bv[3];
-        const float k2 = bias ? s + b : s;
-        const float kk = (k2 != k2) ? -INFINITY : k2;
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-          if (q == j) {
-            sc[q] = s;
-            key[q] = kk;
-          }
-        logits[t * sl + e] = lx;
-      }
+      for (int c = 1; c < 8; ++c) v = lane == c ? d[c] : v;
+      clg[wv][i + lane] = (float)v;
     }
   }
-  topk_rank(sc, key, E, t_ok ? topk : 0, sel_s[wv], sel_i[wv], absent);
+  for (; i < nc; i += 4) {
+    if (lane < 4 && i + lane >= nc) cand[wv][i + lane] = cand[wv][i];
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    double d[4];
+    dots_f64<NQ, 4>(yrow, gate, sg, &cand[wv][i], d);
+    if (lane < 4 && i + lane < nc) {
+      double v = d[0];
+#pragma unroll
+      for (int c = 1; c < 4; ++c) v = lane == c ? d[c] : v;
+      clg[wv][i + lane] = (float)v;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+
+  // each candidate's score and key (fp64 sigmoid, one rounding), its logit stored
+  for (int c = lane; c < nc; c += kWave) {
+    const int e = cand[wv][c];
+    const float lx = clg[wv][c];
+    const float s = (float)(1.0 / (1.0 + exp(-(double)lx)));
+    const float k2 = bias ? s + bias[e] : s;
+    const float kk = (k2 != k2) ? -INFINITY : k2;
+    logits[t * sl + e] = lx;
+    clg[wv][c] = s;
+    cord[wv][c] = ((uint64_t)key_order(kk) << 32) | (uint32_t)(0xffff - e);
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+
+  // slot of each candidate: the number of candidates ahead of it under (key descending,
+  // expert ascending); the top k take slots 0 .. k-1
+  for (int c = lane; c < nc; c += kWave) {
+    const uint64_t me = cord[wv][c];
+    int rank = 0;
+    for (int c2 = 0; c2 < nc; ++c2) rank += cord[wv][c2] > me ? 1 : 0;
+    if (rank < topk) {
+      sel_s[wv][rank] = clg[wv][c];
+      sel_i[wv][rank] = cand[wv][c];
+    }
+  }
   __syncthreads();
   if (t_ok && lane < topk) {
     float w;
@@ -405,7 +500,8 @@ __global__ __launch_bounds__(256) void router_select_kernel(
 // K split for T tokens: about 256 workgroups (one per CU), at most 32 slices, each a
 // multiple of 64 k
 int select_ks(int T, int H) {
-  const int tblocks = (T + kTok - 1) / kTok;
+  const int tok = approx_tok(T);
+  const int tblocks = (T + tok - 1) / tok;
   int ks = 1;
   while (tblocks * ks < 256 && ks < 32 && (H % (64 * ks * 2)) == 0) ks *= 2;
   return ks;
@@ -418,7 +514,7 @@ namespace glm52 {
 int64_t router_select_workspace_bytes(int T, int H, int E) {
   if (T <= 0 || H <= 0 || E <= 0) return 0;
   const int ks = select_ks(T, H);
-  int64_t b = (int64_t)ks * E * 4 + 256;
+  int64_t b = (int64_t)ks * (E + T) * 4 + 256;
   if (ks > 1) b += (int64_t)ks * T * E * 4;
   return b;
 }
@@ -438,26 +534,32 @@ int launch_router_select(const uint16_t* y, int64_t sy, const uint16_t* gate, in
       (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return GLM52_EINVAL;
   float* ssw = static_cast<float*>(workspace);
+  float* ssy = ssw + (int64_t)ks * E;
   float* part = ks > 1 ? reinterpret_cast<float*>(
-                             (reinterpret_cast<uintptr_t>(ssw + (int64_t)ks * E) + 255) & ~uintptr_t(255))
+                             (reinterpret_cast<uintptr_t>(ssy + (int64_t)ks * T) + 255) & ~uintptr_t(255))
                        : nullptr;
-  dim3 grid((T + kTok - 1) / kTok, ks);
-  router_approx_kernel<<<grid, 256, 0, st>>>(y, sy, gate, sg, T, H, E, ks > 1 ? part : logits,
-                                             ks > 1 ? (int64_t)E : sl, ssw);
+  const int tok = approx_tok(T);
+  const unsigned grid = (unsigned)(((T + tok - 1) / tok) * ks);
+  if (tok == 128)
+    router_approx_kernel<128><<<grid, 64 * kWaves, 0, st>>>(
+        y, sy, gate, sg, T, H, E, ks, ks > 1 ? part : logits, ks > 1 ? (int64_t)E : sl, ssw, ssy);
+  else
+    router_approx_kernel<64><<<grid, 64 * kWaves, 0, st>>>(
+        y, sy, gate, sg, T, H, E, ks, ks > 1 ? part : logits, ks > 1 ? (int64_t)E : sl, ssw, ssy);
   hipError_t err = hipGetLastError();
   if (err != hipSuccess) return (int)err;
   const unsigned nb = (unsigned)((T + 3) / 4);
   switch (H / 512) {
     case 8:
-      router_select_kernel<8><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, bias, logits,
+      router_select_kernel<8><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
                                                   sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
       break;
     case 12:
-      router_select_kernel<12><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, bias, logits,
+      router_select_kernel<12><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
                                                    sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
       break;
     default:
-      router_select_kernel<16><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, bias, logits,
+      router_select_kernel<16><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
                                                    sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
       break;
   }

@@ -630,10 +630,12 @@ def test_merge_resadd(gpu, round_mid):
 # ------------------------------------------------------------------ router, bounded path
 def select_bound(y_o, gate, logits_exact):
     """The error bound the bounded router promises for every logit it does not recompute:
-    1.25 * 2^-16 * ||y_t|| ||w_e|| + 2^-21 |L| (plus a hair for the fp32 of L)."""
+    1.375 * 2^-16 * ||y_t|| ||w_e|| + 2^-24 |L~| (chains of eight MFMAs, at most 64 chain
+    sums per K slice in fp32, one rounding of L~), taken here with 2^-20 |L| for the last
+    term."""
     yn = np.sqrt((y_o.double().numpy() ** 2).sum(1))[:, None]
     wn = np.sqrt((gate.double().numpy() ** 2).sum(1))[None, :]
-    return 1.25 * 2.0 ** -16 * yn * wn + 2.0 ** -20 * np.abs(logits_exact) + 1e-30
+    return 1.375 * 2.0 ** -16 * yn * wn + 2.0 ** -20 * np.abs(logits_exact) + 1e-30
 
 
 def run_router_rows(gpu, y, gate, bias, topk=8):

@@ -125,7 +125,10 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
 def test_router_select_workspace_query():
     q = lambda t: _lib.query("glm52_router_select_workspace_bytes", t, 6144, 256)  # noqa: E731
     assert q(16) == 0  # decode keeps the exact rows mapping
-    # 16384 tokens: 256 blocks of 64 tokens, no K split: the gate rows' sums of squares only
-    assert q(16384) == 256 * 4 + 256
-    # 8192 tokens: 128 token blocks x 2 K slices, fp32 partials
-    assert q(8192) == 2 * 256 * 4 + 256 + 2 * 8192 * 256 * 4
+    # per K slice: the gate rows' and the token rows' sums of squares; with a K split also
+    # the fp32 partial logits.  32768 tokens: 256 blocks of 128 tokens, no K split
+    assert q(32768) == (256 + 32768) * 4 + 256
+    # 8192 tokens: 64 blocks of 128 tokens x 4 K slices
+    assert q(8192) == 4 * (256 + 8192) * 4 + 256 + 4 * 8192 * 256 * 4
+    # 2048 tokens: 32 blocks of 64 tokens x 8 K slices
+    assert q(2048) == 8 * (256 + 2048) * 4 + 256 + 8 * 2048 * 256 * 4
