@@ -413,6 +413,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     const int xi = it / 8 - per_xcd;  // >= 0: an item of the extra expert
     const bool xs = xi >= 0;
     int pid_n, row0, e;
+    bool w_once;  // the W tile is streamed by this item only: non-temporal loads
     if (!xs) {
       const int L = (it % 8) * per_xcd + it / 8;
       if (L >= items) continue;
@@ -423,6 +424,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       while (mb > 0 && p.eids[mb - 1] == eb) --mb;
       while (me < num_m && p.eids[me] == eb) ++me;
       const int cnt = me - mb;
+      w_once = cnt == 1;
       const int local = L - mb * num_n;
       pid_n = local / cnt;
       const int pid_m = mb + local % cnt;
@@ -435,6 +437,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       pid_n = Lx / nbx;
       row0 = (Lx % nbx) * MT;
       e = 0;
+      w_once = nbx == 1;
     }
     const int n0 = pid_n * NO;
     const int P = pid_n / SPLIT, sub = pid_n % SPLIT;  // the packed 512-row tile and half
@@ -487,7 +490,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
         const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * (kPackStage / 2) : wexp + kc;
-        dma16s(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
+        if (w_once)
+          dma16s_nt(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
+        else
+          dma16s(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
       } else {
         const int j = i - WI;
         dma16s(Ab + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
