@@ -64,6 +64,7 @@ struct RouteLds {
   float score[RT][kMaxE];
   float sel_s[RT][8];
   int sel_i[RT][8];
+  uint64_t cand[RT][32];  // each wave's top-k keys (slot wave * 8 + its rank), zero-padded
   int ids[RSLOT];
   int blk_e[RSLOT];      // expert of layout block b
   int blk_n[RSLOT];      // its id count (<= RT)
@@ -329,14 +330,41 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       }
     }
     __syncthreads();
-    // slot of expert tid = the number of experts whose key integer is larger
-    for (int t = 0; t < T; ++t) {
-      if (tid < E) {
+    // slot of expert tid = the number of experts whose key integer is larger.  First the
+    // rank inside the wave's 64 experts; the wave's top k go to cand.  A key outside its
+    // wave's top k has at least k larger keys, and for a key inside the global top k every
+    // larger key is in its own wave's top k: so the global slots are the ranks among the
+    // (at most 32) listed keys, and every other key ranks k or more there.
+    int wrank[RT];
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      wrank[t] = kMaxE;
+      if (t < T) {
+        if (lane < 8) rs.cand[t][wv * 8 + lane] = 0ull;  // below every key
+        if (tid < E) {
+          const uint64_t k = rs.key[t][tid];
+          const int e1 = min(E, (wv + 1) * kWave);
+          int rank = 0;
+#pragma unroll 8
+          for (int e2 = wv * kWave; e2 < e1; e2 += 2) {
+            const ulonglong2 q = *reinterpret_cast<const ulonglong2*>(&rs.key[t][e2]);
+            rank += q.x > k ? 1 : 0;
+            rank += q.y > k ? 1 : 0;
+          }
+          wrank[t] = rank;
+          if (rank < topk) rs.cand[t][wv * 8 + rank] = k;
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < RT; ++t) {
+      if (t < T && wrank[t] < topk) {
         const uint64_t k = rs.key[t][tid];
         int rank = 0;
-#pragma unroll 8
-        for (int e2 = 0; e2 < E; e2 += 2) {
-          const ulonglong2 q = *reinterpret_cast<const ulonglong2*>(&rs.key[t][e2]);
+#pragma unroll
+        for (int c = 0; c < 32; c += 2) {
+          const ulonglong2 q = *reinterpret_cast<const ulonglong2*>(&rs.cand[t][c]);
           rank += q.x > k ? 1 : 0;
           rank += q.y > k ? 1 : 0;
         }
