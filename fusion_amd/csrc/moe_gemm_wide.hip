@@ -485,18 +485,22 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 
     // the previous item's output stores and loads are done before this item's are counted
     GLM52_WAIT_VMCNT(0);
+    // Past the last stage the loads keep their count (the waits stay constant) but every
+    // lane reads the same 16 bytes, one cache line per instruction, into the free buffer.
     auto issue_one = [&](int i, int kt) {  // load instruction i of stage kt (clamped)
+      const bool past = kt >= nk;  // wave-uniform
       const int kc = min(kt, nk - 1) * BKS;
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
         const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * (kPackStage / 2) : wexp + kc;
+        const uint32_t vo = past ? 0u : wvoff[i];
         if (w_once)
-          dma16s_nt(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
+          dma16s_nt(src, vo, sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
         else
-          dma16s(src, wvoff[i], sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
+          dma16s(src, vo, sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
       } else {
         const int j = i - WI;
-        dma16s(Ab + kc, avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
+        dma16s(Ab + kc, past ? 0u : avoff[j], sb + (uint32_t)((NTW + wvu * (MT / 4) + j * RPI) * BKS * 2));
       }
     };
 
