@@ -672,6 +672,28 @@ def test_router_bounded_path_bitwise(gpu, T, bias):
     assert ratio.max() <= 1.0
 
 
+@pytest.mark.parametrize("T,H", [(4133, 6144), (300, 4096), (1100, 4096), (300, 8192),
+                                 (4100, 8192)])
+def test_router_bounded_path_shapes(gpu, T, H):
+    """The bounded router at the other hidden sizes it serves (H = 4096, 8192: 8 and 16
+    chunks of 512 k per lane) and at ragged token counts on both token tiles (64 below
+    4096 tokens, 128 from there; K split 8 or 4 ways): ids and weights bit for bit against
+    the exact rule, selected logits exact, the others within the proven bound."""
+    say(f"bounded router T={T} H={H}")
+    g = torch.Generator().manual_seed(7000 + T + H)
+    y = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gate = (torch.randn(256, H, generator=g) * 0.02).to(torch.bfloat16)
+    bias = torch.randn(256, generator=g) * 0.01
+    lg, w, ids = run_router_rows(gpu, y, gate, bias)
+    lg_o, w_o, ids_o = O.router_exact(y, gate.t().contiguous(), bias.numpy())
+    assert np.array_equal(ids, ids_o)
+    assert np.array_equal(w, w_o)
+    sel = np.take_along_axis(lg, ids_o.astype(np.int64), 1)
+    assert np.array_equal(sel, np.take_along_axis(lg_o, ids_o.astype(np.int64), 1))
+    ratio = np.abs(lg.astype(np.float64) - lg_o) / select_bound(y, gate, lg_o)
+    assert ratio.max() <= 1.0
+
+
 def test_router_bounded_path_ties_and_nan(gpu):
     """Exact ties above the cut (16 identical gate rows lifted by the bias: the lower
     indices win), a token of NaN (every key -inf: ids 0..7, NaN weights, as the exact
