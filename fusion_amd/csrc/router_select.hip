@@ -50,7 +50,6 @@ constexpr int kGateIps = kMaxE / (8 * kWaves);  // loads per wave and stage: 8 r
 // workgroups for the smaller batches)
 constexpr int kBigTokT = 4096;
 inline int approx_tok(int T) { return T >= kBigTokT ? 128 : 64; }
-constexpr int kMaxH = 8192;
 
 GLM52_DEV float sumsq8(const uint4& v) {
   float f[8];
@@ -61,11 +60,12 @@ GLM52_DEV float sumsq8(const uint4& v) {
   return s;
 }
 
-// grid = ceil(T / 128) * KS; block = 512.  Wave w computes expert blocks 2 (w % 4) + f
-// (of 32) against token blocks 2 (w / 4) + j, f, j in {0, 1}.  out: KS == 1: L~ into logits [T, E] (row stride
-// so); else fp32 partials part[ks][T][E].  ssw[ks][E] / ssy[ks][T]: the gate rows' / the
-// token rows' sums of squares over slice ks (fp32, one chain of at most H / 2 fused
-// multiply-adds per lane: within 2^-11 relative of the exact sums).
+// grid = ceil(T / TOK) * KS; block = 512.  With TB = TOK / 64 token blocks (of 32) per
+// wave, wave w computes expert blocks 2 (w % 4) + f (of 32, f < 2) against token blocks
+// TB (w / 4) + j (j < TB).  out: KS == 1: L~ into logits [T, E] (row stride so); else
+// fp32 partials part[ks][T][E].  ssw[ks][E] / ssy[ks][T]: the gate rows' / the token rows'
+// sums of squares over slice ks (fp32, one chain of at most H / 2 fused multiply-adds per
+// lane: within 2^-11 relative of the exact sums).
 template <int TOK>
 __global__ __launch_bounds__(512) void router_approx_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const uint16_t* __restrict__ gate, int64_t sg,
@@ -115,15 +115,19 @@ __global__ __launch_bounds__(512) void router_approx_kernel(
   }
   const uint32_t ring_base = lds_addr(ring);
 
+  // past the slice's last stage the loads keep their count (the waits stay constant) but
+  // every lane reads the same 16 bytes
   auto issue = [&](int s) {
+    const bool past = s >= nk;  // wave-uniform
     const int kc = kbeg + min(s, nk - 1) * kBk;
     const uint32_t sb = ring_base + (uint32_t)((s % kStages) * kStageElems * 2);
 #pragma unroll
     for (int i = 0; i < kGateIps; ++i)
-      dma16s(gate + kc, goff[i], sb + (uint32_t)((wv * kGateIps + i) * 8 * kBk * 2));
+      dma16s(gate + kc, past ? 0u : goff[i], sb + (uint32_t)((wv * kGateIps + i) * 8 * kBk * 2));
 #pragma unroll
     for (int i = 0; i < kTokIps; ++i)
-      dma16s(ybase + kc, yoff[i], sb + (uint32_t)((kMaxE + (wv * kTokIps + i) * 8) * kBk * 2));
+      dma16s(ybase + kc, past ? 0u : yoff[i],
+             sb + (uint32_t)((kMaxE + (wv * kTokIps + i) * 8) * kBk * 2));
   };
 
   const int eb0 = (wv % 4) * 2, tb0 = (wv / 4) * TB;
