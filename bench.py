@@ -478,6 +478,47 @@ def calibrate(dev) -> list:
                        "us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
                 log(rec)
                 out.append(rec)
+    del buf
+    out.extend(copy_ceiling(dev, flush_buf))
+    return out
+
+
+def copy_ceiling(dev, flush_buf) -> list:
+    """Read + write ceiling for the vector kernels at T = 8192: two plain device copies of a
+    [8192, 6144] bf16 tensor (403 MB moved, the bytes of ResAdd + RMSNorm) against this
+    build's ResAdd + RMSNorm on the same sizes, median of 20 runs after the benchmark's
+    zeroing flush (which leaves the Infinity Cache full of dirty lines) and after a flush
+    followed by a read of the flush buffer (clean lines)."""
+    import torch
+
+    from fusion_amd.kernels import add_rmsnorm as KN
+
+    T, H = 8192, 6144
+    a, b = (torch.randn(T, H, device=dev).to(torch.bfloat16) for _ in range(2))
+    c, d = torch.empty_like(a), torch.empty_like(a)
+    w = torch.ones(H, dtype=torch.bfloat16, device=dev)
+    nbytes = 4 * T * H * 2
+    kinds = {"copy x2": lambda: (c.copy_(a), d.copy_(b)),
+             "add_rmsnorm": lambda: KN.fused_add_rmsnorm(a, b, w, c, d, {"eps": 1e-5})}
+    out = []
+    for flush_kind in ("zero", "zero+read"):
+        for name, fn in kinds.items():
+            ms = []
+            for _ in range(21):
+                flush_buf.zero_()
+                if flush_kind == "zero+read":
+                    flush_buf.sum()
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record()
+                fn()
+                e.record()
+                torch.cuda.synchronize()
+                ms.append(s.elapsed_time(e))
+            med = statistics.median(ms[1:])
+            rec = {"read_write": name, "bytes": nbytes, "flush": flush_kind,
+                   "us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1)}
+            log(rec)
+            out.append(rec)
     return out
 
 
