@@ -81,7 +81,7 @@ def main() -> int:
     import torch
 
     from fusion_amd import roofline as RL
-    from fusion_amd.block import MoEBlock
+    from fusion_amd.block import MoEBlock, PackedExperts
     from fusion_amd.problem import expert_weights, front_end
 
     dev = torch.device("cuda:0")
@@ -99,15 +99,17 @@ def main() -> int:
         del src, dst
     t0 = time.time()
     W = expert_weights(device=dev)
+    # the blocks read one resident layout, packed once here; the row-major set stays for
+    # the reference-API strategies of down_merge_bench and the CPU baseline
+    PW = PackedExperts(W.w13, W.w2, W.w13s, W.w2s)
     torch.cuda.synchronize()
-    log(f"weights ready in {time.time() - t0:.1f}s")
+    log(f"weights ready in {time.time() - t0:.1f}s ({PW.nbytes() / 1e9:.1f} GB packed)")
     flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)  # 1 GiB
     if args.pmc_child:
         T = int(args.tokens.split(",")[0])
         fe = front_end(T, bias="zipf" if T == 8192 else "normal")
         x, r = fe.x.to(dev), fe.r.to(dev)
-        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), W.w13, W.w2,
-                       W.w13s, W.w2s)
+        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), PW)
         blk(x, r)
         torch.cuda.synchronize()
         step = {"w13": blk.w13_step, "w2": blk.w2_step, "block": lambda: blk(x, r)}[args.pmc_step]
@@ -146,8 +148,7 @@ def main() -> int:
         bias = "zipf" if T == 8192 else "normal"
         fe = front_end(T, bias=bias)
         x, r = fe.x.to(dev), fe.r.to(dev)
-        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), W.w13, W.w2,
-                       W.w13s, W.w2s)
+        blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), PW)
         blk(x, r)
         torch.cuda.synchronize()
         loads = torch.bincount(blk.topi.reshape(-1).long(), minlength=blk.E).cpu()
@@ -243,11 +244,13 @@ COPY_KIB = 262144  # the child's plain copies: 256 MiB read and 256 MiB written 
 
 def w13_kernel_name(blk) -> str:
     """The kernel behind `MoEBlock.w13_step` (as the profiler names it)."""
+    pk = "true" if blk.packed else "false"
     if blk.front_fused:
-        return ("moe_gemm_runs_kernel<true, false, true> (routing + routed and shared "
+        return (f"moe_gemm_runs_kernel<true, false, true, {pk}> (routing + routed and shared "
                 "w13 + SwiGLU)")
     if blk.shared_fused:
-        return "moe_gemm_runs_kernel<true, false, false> (routed and shared w13 + SwiGLU)"
+        return (f"moe_gemm_runs_kernel<true, false, false, {pk}> (routed and shared w13 + "
+                "SwiGLU)")
     ntw = 256 if blk.bm == 256 else 512
     return (f"moe_gemm_w512_kernel<{blk.bm}, {ntw}, true, false, true, 0> (routed and shared "
             f"w13 + SwiGLU)")
@@ -359,8 +362,8 @@ def down_merge_bench(blk, W, T: int, n_e: int, timed, steps: int, warmup: int) -
     H, I, k = blk.H, blk.I, blk.topk
     R = T * k
     cfg = {"BLOCK_M": blk.bm}
-    if getattr(blk, "packed", False):
-        cfg["w2_packed"] = blk.w2_p
+    if blk.packed and blk.bm != 16:  # the 512-row mapping of the atomic merge reads it
+        cfg["w2_packed"] = blk.experts.w2
     tw = blk.topw.reshape(-1)
     c3 = torch.empty(R, H, dtype=torch.bfloat16, device=blk.h.device)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=blk.h.device)

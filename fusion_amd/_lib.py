@@ -39,6 +39,9 @@ SIGNATURES: dict[str, list] = {
     "glm52_moe_gemm_route_shared": [_P, _L, _P, _I, _I, _I, _F, _I, _P, _L, _P, _L, _P, _P, _P,
                                     _I, _P, _L, _P, _L, _L, _I, _P, _L, _P, _L, _P, _P, _L, _I,
                                     _I, _P],
+    "glm52_moe_gemm_route_shared_packed": [_P, _L, _P, _I, _I, _I, _F, _I, _P, _L, _P, _L, _P,
+                                           _P, _P, _I, _P, _L, _P, _P, _L, _P, _L, _P, _P, _L,
+                                           _I, _I, _P],
     "glm52_moe_gemm": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                        _I, _I, _P],
     "glm52_moe_gemm_shared": [_P, _L, _I, _P, _L, _L, _I, _P, _L, _P, _P, _P, _P, _I, _I, _I,
@@ -59,6 +62,8 @@ SIGNATURES: dict[str, list] = {
                              _I, _P],
     "glm52_down_token_major": [_P, _L, _P, _L, _L, _P, _P, _L, _I, _I, _P, _L, _P, _L, _P, _L, _P,
                                _L, _I, _I, _I, _P],
+    "glm52_down_token_major_packed": [_P, _L, _P, _P, _P, _L, _I, _I, _P, _L, _P, _P, _L, _P,
+                                      _L, _I, _I, _I, _P],
     "glm52_silu_and_mul": [_P, _L, _P, _L, _I, _I, _P],
     "glm52_moe_sum": [_P, _L, _L, _P, _L, _P, _L, _I, _I, _I, _I, _P],
     "glm52_resadd": [_P, _L, _P, _L, _P, _L, _I, _I, _P],

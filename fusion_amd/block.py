@@ -23,9 +23,12 @@ the routing computed live instead of frozen, and the tail fused):
                                  over all experts, one rounding -- the reference's
                                  token-major strategy #9(b))
 
-At block sizes 64, 128 and 256 (prefill) the four GEMMs read weights packed once in the
-constructor (`pack_w512`: every 32-k stage of a 512-row W tile as 32 KB of contiguous
-memory), which computes the same bits as reading them in place.
+The expert weights are held in one resident layout, packed once at load (`PackedExperts`,
+`pack_w512`: every 32-k stage of a 512-row W tile as 32 KB of contiguous memory), which
+every block size reads: the prefill tiles stage whole 32 KB stages, the decode weight
+stream reads each load slot's 1 KB of 16 rows x 32 k.  The GEMMs compute the same bits as
+on the row-major weights (the token-major tail sums in another order).  `pack=False` (or
+a `variant`) reads the row-major weights in place instead.
 
 Every buffer is allocated once in the constructor (destination passing, as the
 reference's `LayerProblem` does, `glm52/bench/bench_layer.py:316-346`); `forward` only
@@ -41,12 +44,11 @@ from . import config as C
 from . import _lib
 from .dispatch import (DECODE_FRONT_MAX_T, capacity, decode_norm_logits_into,
                        align_workspace, moe_align_block_size_into, route_gateup_shared_into,
-                       topk_align_into)
+                       route_gateup_shared_packed_into, topk_align_into)
 from .kernels import add_rmsnorm as KN
 from .kernels import moe_down_merge as KD
 from .kernels import norm_router as KR
-from .kernels.moe_gateup import (moe_gemm, moe_gemm_packed, moe_gemm_packed_shared,
-                                 moe_gemm_shared, pack_w512)
+from .kernels.moe_gateup import moe_gemm, moe_gemm_packed_shared, moe_gemm_shared, pack_w512
 
 BF16 = torch.bfloat16
 
@@ -90,21 +92,81 @@ def shared_layout(T: int, block_m: int, device) -> tuple[torch.Tensor, torch.Ten
     return sti.to(device), eids.to(device), ntp.to(device)
 
 
-class MoEBlock:
-    def __init__(self, T: int, w_norm, wgt, bias, w13, w2, w13s, w2s, block_m: int | None = None,
-                 shared_block_m: int | None = None, variant: str | None = None,
-                 eps: float = C.RMS_NORM_EPS, scale: float = C.ROUTED_SCALING_FACTOR,
-                 pack: bool = True, token_major: bool | None = None):
-        _lib.require_gpu(w_norm, wgt, bias, w13, w2, w13s, w2s)
-        dev = w13.device
-        self.T = T
+def packed_shapes_ok(T: int, H: int, I: int, block_m: int | None = None,
+                     shared_block_m: int | None = None) -> bool:
+    """Whether the packed mappings cover this block: whole 512-row tiles (I % 256 gated,
+    H % 512 plain); the weight stream (block size 16) reads 512-k stages (H, I % 512); the
+    prefill tiles 64-k pairs of stages; the token-major tail K = I of 1024 or 2048."""
+    bm = block_m or default_block_m(T)
+    sbm = shared_block_m or default_shared_block_m(T)
+    if I % 256 or H % 512:
+        return False
+    if bm == 16:
+        return I % 512 == 0 and (T > DECODE_FRONT_MAX_T or I in (1024, 2048))
+    return bm in (64, 128, 256) and sbm in (64, 128, 256) and I % 64 == 0
+
+
+class PackedExperts:
+    """The routed experts' and the shared expert's w13 and w2 in the one resident layout
+    (`pack_w512`), packed once at load; the row-major tensors may be freed afterwards.
+    w13 [E, 2I, H] (`gate` rows 0 .. I-1, `up` rows I .. 2I-1), w2 [E, H, I]; the shared
+    ones [1, 2I, H] / [2I, H] and [1, H, I] / [H, I]."""
+
+    def __init__(self, w13, w2, w13s, w2s):
+        _lib.require_gpu(w13, w2, w13s, w2s)
         self.E, I2, self.H = w13.shape
         self.I = I2 // 2
+        w13s = w13s if w13s.dim() == 3 else w13s.unsqueeze(0)
+        w2s = w2s if w2s.dim() == 3 else w2s.unsqueeze(0)
+        if tuple(w2.shape) != (self.E, self.H, self.I) or tuple(w13s.shape) != (1, I2, self.H) \
+                or tuple(w2s.shape) != (1, self.H, self.I):
+            raise ValueError("expert weight shapes must be [E, 2I, H], [E, H, I], "
+                             "[1, 2I, H], [1, H, I]")
+        self.device = w13.device
+        self.w13 = pack_w512(w13, self.I, self.I, True)
+        self.w2 = pack_w512(w2, self.H, 0, False)
+        self.w13s = pack_w512(w13s, self.I, self.I, True)
+        self.w2s = pack_w512(w2s, self.H, 0, False)
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * 2 for t in (self.w13, self.w2, self.w13s, self.w2s))
+
+
+class MoEBlock:
+    def __init__(self, T: int, w_norm, wgt, bias, w13, w2=None, w13s=None, w2s=None,
+                 block_m: int | None = None, shared_block_m: int | None = None,
+                 variant: str | None = None, eps: float = C.RMS_NORM_EPS,
+                 scale: float = C.ROUTED_SCALING_FACTOR, pack: bool = True,
+                 token_major: bool | None = None):
+        """w13 is either the row-major [E, 2I, H] tensor (with w2, w13s, w2s) or a
+        `PackedExperts` (w2, w13s, w2s None).  Row-major weights are packed here unless
+        `pack=False` or a `variant` asks for the in-place mappings; the block keeps one
+        layout only, never both."""
+        _lib.require_gpu(w_norm, wgt, bias)
+        self.experts = None
+        if isinstance(w13, PackedExperts):
+            if w2 is not None or w13s is not None or w2s is not None or variant is not None:
+                raise ValueError("with PackedExperts pass no other weights and no variant")
+            self.experts = w13
+        elif pack and variant is None and packed_shapes_ok(T, w13.shape[2], w13.shape[1] // 2,
+                                                           block_m, shared_block_m):
+            self.experts = PackedExperts(w13, w2, w13s, w2s)
+        if self.experts is not None:
+            P = self.experts
+            dev = P.device
+            self.E, self.H, self.I = P.E, P.H, P.I
+            self.w13 = self.w2 = self.w13s = self.w2s = None  # not held
+        else:
+            _lib.require_gpu(w13, w2, w13s, w2s)
+            dev = w13.device
+            self.E, I2, self.H = w13.shape
+            self.I = I2 // 2
+            self.w13, self.w2 = w13, w2
+            self.w13s = w13s if w13s.dim() == 3 else w13s.unsqueeze(0)
+            self.w2s = w2s if w2s.dim() == 3 else w2s.unsqueeze(0)
+        self.T = T
         self.topk = C.TOPK
         self.w_norm, self.wgt, self.bias = w_norm, wgt, bias
-        self.w13, self.w2 = w13, w2
-        self.w13s = w13s if w13s.dim() == 3 else w13s.unsqueeze(0)
-        self.w2s = w2s if w2s.dim() == 3 else w2s.unsqueeze(0)
         self.eps, self.scale = eps, scale
         self.bm = block_m or default_block_m(T)
         self.sbm = shared_block_m or default_shared_block_m(T)
@@ -153,15 +215,12 @@ class MoEBlock:
         self.router_ws = torch.empty(max(need, 8), dtype=torch.uint8, device=dev)
         self.cfg_topk = {"correction_bias": bias, "scale": scale, "workspace": self.router_ws}
         self.graph = None
-        # prefill (block sizes 64, 128, 256): the GEMMs read weights packed once here, every
-        # 32-k stage of a 512-row W tile as 32 KB of contiguous memory (the same bits)
-        self.packed = (pack and variant is None and not self.shared_fused
-                       and self.bm in (64, 128, 256) and self.sbm in (64, 128, 256))
-        if self.packed:
-            self.w13_p = pack_w512(w13, self.I, self.I, True)
-            self.w2_p = pack_w512(w2, self.H, 0, False)
-            self.w13s_p = pack_w512(self.w13s, self.I, self.I, True)
-            self.w2s_p = pack_w512(self.w2s, self.H, 0, False)
+        # the GEMMs read the packed layout at every block size (16: the weight stream over
+        # load slots; 64, 128, 256: the 512-row and 256-row tiles)
+        self.packed = self.experts is not None
+        if self.packed and not (self.shared_fused or (self.bm in (64, 128, 256)
+                                                      and self.sbm in (64, 128, 256))):
+            raise ValueError(f"no packed mapping for block sizes {self.bm} / {self.sbm}")
 
     # ---- the chain -------------------------------------------------------------------
     def front_end(self, x, r):
@@ -190,34 +249,40 @@ class MoEBlock:
         launch (weight streaming and packed prefill), else the routed launch (the shared one
         is in w2_step)."""
         T, I, R = self.T, self.I, self.T * self.topk
-        if self.front_fused:
+        P = self.experts
+        if self.front_fused and self.packed:
+            route_gateup_shared_packed_into(self.logits, self.cfg_topk, self.topw, self.topi,
+                                            self.sti, self.eids, self.ntp, self.y, P.w13,
+                                            self.act, self.y, P.w13s, self.act_s)
+        elif self.front_fused:
             route_gateup_shared_into(self.logits, self.cfg_topk, self.topw, self.topi, self.sti,
                                      self.eids, self.ntp, self.y, self.w13, self.act, self.y,
                                      self.w13s, self.act_s)
+        elif self.packed:
+            # routed and shared w13 in one launch: the weight stream at block size 16, the
+            # tiles above (the shared expert's items after each XCD's routed ones)
+            moe_gemm_packed_shared(self.y, self.topk, P.w13, self.act, None, self.sti,
+                                   self.eids, self.ntp, R, I, True, self.cfg_r, self.y,
+                                   P.w13s, self.act_s)
         elif self.shared_fused:
             moe_gemm_shared(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids,
                             self.ntp, R, I, I, True, self.cfg_r, self.y, self.w13s, self.act_s)
-        elif self.packed:
-            # routed and shared w13 in one launch (the shared expert's items after each
-            # XCD's routed ones)
-            moe_gemm_packed_shared(self.y, self.topk, self.w13_p, self.act, None, self.sti,
-                                   self.eids, self.ntp, R, I, True, self.cfg_r, self.y,
-                                   self.w13s_p, self.act_s)
         else:
             moe_gemm(self.y, self.topk, self.w13, self.act, None, self.sti, self.eids, self.ntp,
                      R, I, I, True, self.cfg_r)
 
     def w2_step(self):
         T, H, I, R = self.T, self.H, self.I, self.T * self.topk
+        if self.packed:
+            P = self.experts
+            moe_gemm_packed_shared(self.act, 1, P.w2, self.ybuf, self.topw.view(-1), self.sti,
+                                   self.eids, self.ntp, R, H, False, self.cfg_r, self.act_s,
+                                   P.w2s, self.s_out)
+            return
         if self.shared_fused:
             moe_gemm_shared(self.act, 1, self.w2, self.ybuf, self.topw.view(-1), self.sti,
                             self.eids, self.ntp, R, H, 0, False, self.cfg_r, self.act_s, self.w2s,
                             self.s_out)
-            return
-        if self.packed:
-            moe_gemm_packed_shared(self.act, 1, self.w2_p, self.ybuf, self.topw.view(-1),
-                                   self.sti, self.eids, self.ntp, R, H, False, self.cfg_r,
-                                   self.act_s, self.w2s_p, self.s_out)
             return
         moe_gemm(self.y, 1, self.w13s, self.act_s, None, self.ssti, self.seids, self.sntp,
                  T, I, I, True, self.cfg_s)
@@ -232,6 +297,11 @@ class MoEBlock:
 
     def tail(self):
         """Steps 7-9: the token-major GEMV at decode sizes, else w2 then the merge."""
+        if self.token_major and self.packed:
+            P = self.experts
+            KD.launch_down_token_major_packed(self.act, P.w2, self.out, self.topw, self.topi,
+                                              self.h, self.topk, True, self.act_s, P.w2s)
+            return
         if self.token_major:
             KD.launch_down_token_major(self.act, self.w2, self.out, self.topw, self.topi, self.h,
                                        self.topk, {}, True, self.act_s, self.w2s)

@@ -114,6 +114,108 @@ __global__ __launch_bounds__(256) void down_tokmaj_kernel(
   }
 }
 
+// The same sum on packed weights (glm52_pack_w512 of w2 for N plain outputs).  The 16 rows
+// of packed load slot q of 512-row tile P are rows P * 512 + (q / 8) * 128 + (q % 8 / 2) * 32
+// + (q % 2) * 8 + phi32(p), p = 0 .. 15; the slot holds their K / 32 stages one after the
+// other, 1 KB each, lane l's 16 bytes holding row p = l / 4, 8-k chunk (l % 4) ^ (p / 4 % 4).
+// Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token t: wave w takes stages
+// 2 QS w .. 2 QS w + 2 QS - 1 as two pieces of QS (QS KB of contiguous memory each), every
+// load reads one stage's whole 1 KB, and a lane keeps one fp32 partial of its row over all
+// pieces.  The 4 lanes of a row, then the 4 waves, meet in a fixed order.  The pieces flow
+// through two register buffers, so a wave has two pieces' loads in flight; four waves per
+// workgroup let two workgroups share a CU (about 210 VGPRs), so at T = 1 and N = 6144 the
+// 384 workgroups run in a single round.
+template <int QS>
+__global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
+    const uint16_t* __restrict__ a, int64_t sam, const uint16_t* __restrict__ w2p,
+    const float* __restrict__ topw, const int32_t* __restrict__ topi, int64_t stk, int topk,
+    int E, const uint16_t* __restrict__ a_s, int64_t sas, const uint16_t* __restrict__ w2sp,
+    const uint16_t* __restrict__ res, int64_t srm, uint16_t* __restrict__ out, int64_t som,
+    int N) {
+  __shared__ float red[4][16];
+  const int lane = threadIdx.x % kWave;
+  const int wv = threadIdx.x / kWave;
+  const int t = blockIdx.y;
+  const int P = blockIdx.x >> 5, q = blockIdx.x & 31;
+  constexpr int NK = 8 * QS;                // 32-k stages of a row (K / 32)
+  const int num_n512 = N / 512;
+  const int pr = lane >> 2;                      // the lane's row in the slot
+  const int kc = (lane & 3) ^ ((pr >> 2) & 3);   // and its 8-k chunk of every stage
+  const int64_t toff = P * packed_tile_elems(NK) + q * packed_slot_elems(NK) + lane * 8;
+  const int npieces = 2 * (topk + (w2sp ? 1 : 0));
+
+  // piece c: half c % 2 of the wave's stages of unit c / 2 -- routed expert u of the
+  // token, or (u == topk) the shared expert
+  auto load_piece = [&](int c, uint4 (&wr)[QS], uint4 (&ar)[QS], float& wk) {
+    const int u = c >> 1;
+    const int kt0 = (2 * wv + (c & 1)) * QS;
+    const uint16_t* wb = nullptr;
+    const uint16_t* arow = nullptr;
+    wk = 0.f;
+    if (u < topk) {
+      const int e = topi[(int64_t)t * stk + u];
+      if (e >= 0 && e < E) {  // an id outside [0, E) contributes nothing
+        wb = w2p + (int64_t)e * num_n512 * packed_tile_elems(NK) + toff;
+        arow = a + ((int64_t)t * topk + u) * sam;
+        wk = topw[(int64_t)t * stk + u];
+      }
+    } else {
+      wb = w2sp + toff;
+      arow = a_s + (int64_t)t * sas;
+      wk = 1.f;
+    }
+#pragma unroll
+    for (int i = 0; i < QS; ++i)
+      ar[i] = arow ? ldg(arow + (kt0 + i) * 32 + kc * 8) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < QS; ++i)
+      wr[i] = wb ? ldg_nt(wb + (kt0 + i) * 512) : make_uint4(0, 0, 0, 0);
+  };
+
+  float acc = 0.f;
+  auto fma_piece = [&](const uint4 (&wr)[QS], const uint4 (&ar)[QS], float wk) {
+    float pd = 0.f;
+#pragma unroll
+    for (int i = 0; i < QS; ++i) {
+      float af[8], wf[8];
+      unpack8(ar[i], af);
+      unpack8(wr[i], wf);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pd = fmaf(af[j], wf[j], pd);
+    }
+    acc = fmaf(wk, pd, acc);
+  };
+
+  uint4 wc[QS], wn[QS], ac[QS], an[QS];
+  float kc_w, kn_w;
+  load_piece(0, wc, ac, kc_w);
+  for (int c = 0; c < npieces; ++c) {
+    const bool more = c + 1 < npieces;
+    if (more) load_piece(c + 1, wn, an, kn_w);
+    fma_piece(wc, ac, kc_w);
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < QS; ++i) {
+        ac[i] = an[i];
+        wc[i] = wn[i];
+      }
+      kc_w = kn_w;
+    }
+  }
+
+  acc += __shfl_xor(acc, 1, kWave);
+  acc += __shfl_xor(acc, 2, kWave);
+  if ((lane & 3) == 0) red[wv][pr] = acc;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    const int i = threadIdx.x;
+    const float v0 = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
+    const int n = P * 512 + (q >> 3) * 128 + ((q & 7) >> 1) * 32 + (q & 1) * 8 + phi32(i);
+    const float v = res ? v0 + bf16_to_f32(res[(int64_t)t * srm + n]) : v0;
+    out[(int64_t)t * som + n] = f32_to_bf16(v);
+  }
+}
+
 bool al16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -160,5 +262,46 @@ extern "C" int glm52_down_token_major(const void* a, int64_t stride_am, const vo
     down_tokmaj_kernel<4><<<grid, 256, 0, stream>>>(aa, stride_am, ww, stride_we, stride_wn,
         topk_weights, topk_ids, stride_tk, top_k, num_experts, as, stride_as, ws, stride_ws, rr,
         stride_rm, oo, stride_om, N);
+  GLM52_RETURN_LAUNCH();
+}
+
+// glm52_down_token_major on packed weights: w2_packed = glm52_pack_w512 of w2 ([E, N, K],
+// plain, n_out = N), w2_shared_packed (may be null) the same of the [1, N, K] shared w2.
+// N must be a multiple of 512, K 1024 or 2048.  Same sum; the adds run in another order.
+extern "C" int glm52_down_token_major_packed(const void* a, int64_t stride_am,
+                                             const void* w2_packed, const float* topk_weights,
+                                             const int32_t* topk_ids, int64_t stride_tk,
+                                             int top_k, int num_experts, const void* a_shared,
+                                             int64_t stride_as, const void* w2_shared_packed,
+                                             const void* residual, int64_t stride_rm, void* out,
+                                             int64_t stride_om, int T, int N, int K,
+                                             hipStream_t stream) {
+  if (T < 0 || T > 65535 || N <= 0 || (N % 512) || top_k < 1 || num_experts < 1 ||
+      stride_tk < top_k)
+    return GLM52_EINVAL;
+  if (K != 1024 && K != 2048) return GLM52_EUNSUPPORTED;
+  if (T == 0) return GLM52_OK;
+  if (!a || !w2_packed || !topk_weights || !topk_ids || !out) return GLM52_EINVAL;
+  if (!al16(a) || !al16(w2_packed) || (stride_am % 8) || stride_am < K || stride_om < N)
+    return GLM52_EINVAL;
+  if (w2_shared_packed && (!a_shared || !al16(a_shared) || !al16(w2_shared_packed) ||
+                           (stride_as % 8) || stride_as < K))
+    return GLM52_EINVAL;
+  if (residual && stride_rm < N) return GLM52_EINVAL;
+  const dim3 grid(N / 16, T);
+  auto* aa = static_cast<const uint16_t*>(a);
+  auto* ww = static_cast<const uint16_t*>(w2_packed);
+  auto* as = static_cast<const uint16_t*>(a_shared);
+  auto* ws = static_cast<const uint16_t*>(w2_shared_packed);
+  auto* rr = static_cast<const uint16_t*>(residual);
+  auto* oo = static_cast<uint16_t*>(out);
+  if (K == 1024)
+    down_tokmaj_packed_kernel<4><<<grid, 256, 0, stream>>>(aa, stride_am, ww, topk_weights,
+        topk_ids, stride_tk, top_k, num_experts, as, stride_as, ws, rr, stride_rm, oo,
+        stride_om, N);
+  else
+    down_tokmaj_packed_kernel<8><<<grid, 256, 0, stream>>>(aa, stride_am, ww, topk_weights,
+        topk_ids, stride_tk, top_k, num_experts, as, stride_as, ws, rr, stride_rm, oo,
+        stride_om, N);
   GLM52_RETURN_LAUNCH();
 }

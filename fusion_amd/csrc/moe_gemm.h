@@ -87,6 +87,16 @@ GLM52_DEV uint32_t lds_addr(const uint16_t* p) {
 // s_waitcnt vmcnt(n): every older vector-memory load of this wave has completed.
 #define GLM52_WAIT_VMCNT(n) asm volatile("s_waitcnt vmcnt(%0)" : : "n"(n) : "memory")
 
+// The packed weight layout (glm52_pack_w512).  W row (inside its 32-row group) held at
+// LDS row p of the 512-row tile; load slot w * 8 + i of a tile holds 16 rows of one 32-row
+// group (rows phi32(p) + 8 (i % 2) for p = 0 .. 15), each 32-k stage of them as 1 KB, lane
+// l's 16 bytes being row p = l / 4, 8-k chunk (l % 4) ^ ((p / 4) % 4); a slot's nk = K / 32
+// stages follow each other (nk KB per slot), and a tile's 32 slots likewise.
+GLM52_DEV int phi32(int p) { return ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); }
+// elements of one packed slot and of one packed 512-row tile, for nk 32-k stages
+__host__ __device__ inline int64_t packed_slot_elems(int nk) { return (int64_t)nk * 512; }
+__host__ __device__ inline int64_t packed_tile_elems(int nk) { return 32 * packed_slot_elems(nk); }
+
 struct GemmArgs {
   const uint16_t* A;
   int64_t sam;

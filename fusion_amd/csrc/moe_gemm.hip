@@ -503,11 +503,11 @@ extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row
                                      int gated, hipStream_t stream) {
   if (!a || !w_packed || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded)
     return GLM52_EINVAL;
-  if ((block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
+  if ((block_m != 16 && block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
       (capacity % block_m) != 0)
     return GLM52_EINVAL;
-  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 || (k % 64) != 0 ||
-      a_row_div <= 0)
+  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 ||
+      (k % (block_m == 16 ? 512 : 64)) != 0 || a_row_div <= 0)
     return GLM52_EINVAL;
   if (!al16(a) || !al16(w_packed) || (stride_am % 8) || !al16(c) || (stride_cm % 8))
     return GLM52_EINVAL;
@@ -520,6 +520,8 @@ extern "C" int glm52_moe_gemm_packed(const void* a, int64_t stride_am, int a_row
              num_tokens_post_padded, block_m, n_out, k, num_valid_tokens, 4, 64,
              nullptr, 0, nullptr, nullptr, 0, 0, ab, 0};
   g.Wp = static_cast<const uint16_t*>(w_packed);
+  if (block_m == 16)  // the contiguous-run weight stream on the packed load slots
+    return launch_runs(g, capacity, gated != 0, topk_weights != nullptr, false, stream);
   return launch_wide512(g, capacity, gated != 0, topk_weights != nullptr, stream);
 }
 
@@ -537,11 +539,11 @@ extern "C" int glm52_moe_gemm_packed_shared(
   if (!a || !w_packed || !c || !sorted_token_ids || !expert_ids || !num_tokens_post_padded ||
       !a_shared || !w_shared_packed || !c_shared || shared_rows < 0)
     return GLM52_EINVAL;
-  if ((block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
+  if ((block_m != 16 && block_m != 64 && block_m != 128 && block_m != 256) || capacity < 0 ||
       (capacity % block_m) != 0)
     return GLM52_EINVAL;
-  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 || (k % 64) != 0 ||
-      a_row_div <= 0)
+  if (n_out <= 0 || (n_out % (gated ? 256 : 512)) != 0 || k <= 0 ||
+      (k % (block_m == 16 ? 512 : 64)) != 0 || a_row_div <= 0)
     return GLM52_EINVAL;
   if (!al16(a) || !al16(w_packed) || (stride_am % 8) || !al16(c) || (stride_cm % 8) ||
       !al16(a_shared) || (stride_as % 8) || !al16(w_shared_packed) || !al16(c_shared) ||
@@ -559,6 +561,8 @@ extern "C" int glm52_moe_gemm_packed_shared(
              static_cast<const uint16_t*>(w_shared_packed), static_cast<uint16_t*>(c_shared),
              stride_cs, shared_rows, ab, axb};
   g.Wp = static_cast<const uint16_t*>(w_packed);
+  if (block_m == 16)  // the contiguous-run weight stream on the packed load slots
+    return launch_runs(g, capacity, gated != 0, topk_weights != nullptr, false, stream);
   return launch_wide512(g, capacity, gated != 0, topk_weights != nullptr, stream);
 }
 
@@ -641,6 +645,39 @@ extern "C" int glm52_moe_gemm_route_shared(
              T, 0, 0,
              logits, stride_l, bias, T, E, topk, norm_prob, scale, topw, stride_w, topi, stride_i,
              sorted_token_ids, expert_ids, num_tokens_post_padded, capacity};
+  return launch_runs(g, capacity, true, false, true, stream);
+}
+
+// glm52_moe_gemm_route_shared on packed weights (glm52_pack_w512 of w13 for n_out gated
+// outputs, and of the [1, 2 n_out, K] shared w13): the same routing, layout and bits.
+extern "C" int glm52_moe_gemm_route_shared_packed(
+    const float* logits, int64_t stride_l, const float* bias, int T, int E, int topk,
+    float scale, int norm_prob, float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i,
+    int32_t* sorted_token_ids, int32_t* expert_ids, int32_t* num_tokens_post_padded,
+    int capacity, const void* a, int64_t stride_am, const void* w_packed, void* c,
+    int64_t stride_cm, const void* a_shared, int64_t stride_as, const void* w_shared_packed,
+    void* c_shared, int64_t stride_cs, int n_out, int k, hipStream_t stream) {
+  if (!logits || !topw || !topi || !sorted_token_ids || !expert_ids || !num_tokens_post_padded ||
+      !a || !w_packed || !c || !a_shared || !w_shared_packed || !c_shared)
+    return GLM52_EINVAL;
+  if (T < 1 || T > 4 || E < 1 || topk < 1 || topk > 8 || topk > E || stride_l < E ||
+      stride_w < topk || stride_i < topk || capacity < 0 || (capacity % 16))
+    return GLM52_EINVAL;
+  if (!al16(logits) || (stride_l % 4) || (bias && !al16(bias))) return GLM52_EINVAL;
+  if (n_out <= 0 || (n_out % 256) != 0 || k <= 0 || (k % 512) != 0) return GLM52_EINVAL;
+  if (!al16(a) || !al16(w_packed) || !al16(w_shared_packed) || !al16(a_shared) ||
+      (stride_am % 8) || (stride_as % 8) || !c_ok8(c, stride_cm) || !c_ok8(c_shared, stride_cs))
+    return GLM52_EINVAL;
+  GemmArgs g{static_cast<const uint16_t*>(a), stride_am, topk,
+             static_cast<const uint16_t*>(w_packed), 0, 0, n_out,
+             static_cast<uint16_t*>(c), stride_cm, nullptr, sorted_token_ids, expert_ids,
+             num_tokens_post_padded, 16, n_out, k, T * topk, 4, 64,
+             static_cast<const uint16_t*>(a_shared), stride_as,
+             static_cast<const uint16_t*>(w_shared_packed), static_cast<uint16_t*>(c_shared),
+             stride_cs, T, 0, 0,
+             logits, stride_l, bias, T, E, topk, norm_prob, scale, topw, stride_w, topi, stride_i,
+             sorted_token_ids, expert_ids, num_tokens_post_padded, capacity};
+  g.Wp = static_cast<const uint16_t*>(w_packed);
   return launch_runs(g, capacity, true, false, true, stream);
 }
 

@@ -82,6 +82,14 @@ GLM52_DEV int sload_i32(const void* base, int idx) {
   return v;
 }
 
+// A wave-uniform pointer the compiler keeps in SGPRs (the base operand of dma16s).
+GLM52_DEV const uint16_t* uniform_ptr(const uint16_t* q) {
+  const uint64_t v = reinterpret_cast<uint64_t>(q);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return reinterpret_cast<const uint16_t*>(((uint64_t)hi << 32) | lo);
+}
+
 typedef int sint4_t __attribute__((ext_vector_type(4)));
 
 // Expert id eids[b] and the four slot entries sti[s .. s+3] (s a multiple of 4) in one
@@ -153,7 +161,7 @@ GLM52_DEV void wait_vmcnt_at_most(int n) {
   }
 }
 
-template <bool GATED, bool WEIGHTED, bool ROUTE>
+template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
   __shared__ float red[2][4][4][kWave];  // partial sums of the last two items, by wave
@@ -172,6 +180,15 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   const int num_n = p.n_out / NOC;
   const int x_items = xm * num_n;  // the extra expert's items come first
   const int nks = p.K / KS;
+  // packed weights: the item's 512-row tile and its 32-k stages
+  constexpr int NO512 = GATED ? 256 : 512;
+  const int num_n512 = p.n_out / NO512;
+  const int nk32 = p.K / 32;
+  // read once here in the packed instances, whose register pressure otherwise keeps these
+  // fields of p in scratch (every scratch load waits for all loads in flight)
+  const uint16_t* const pw_r = p.Wp;
+  const uint16_t* const pw_x = p.Wx;
+  const int nvalid = PACKED ? __builtin_amdgcn_readfirstlane(p.num_valid) : p.num_valid;
   int num_m = ROUTE ? 0 : sload_i32(p.ntp, 0) / 16;
   int items = (xm + num_m) * num_n;
   const uint32_t ring_base = lds_addr(ring);
@@ -195,6 +212,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // ---- load side: the wave's 4 W rows and its real token rows (da_n of 4) of the item
   // being loaded; the item's token ids (and weights) go to the LDS ring for its epilogue
   const uint16_t* dw[4];
+  uint32_t wvo = 0;  // packed: the lane's byte offset inside the item's load slot(s)
   const uint16_t* da[4];
   int da_n = 0;
   auto dma_setup = [&](int it) {
@@ -206,25 +224,47 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     // the block's expert and the wave's four slot entries: from LDS in routing mode, else
     // in one scalar round trip
     int e = 0;
-    int fr[4] = {p.num_valid, p.num_valid, p.num_valid, p.num_valid};
+    const int nv = PACKED ? nvalid : p.num_valid;
+    int fr[4] = {nv, nv, nv, nv};
     if (!extra) {
       if constexpr (ROUTE) {
         e = __builtin_amdgcn_readfirstlane(rs.blk_e[m - xm]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int tr = wvu * 4 + i;
-          fr[i] = __builtin_amdgcn_readfirstlane(tr < rs.blk_n[m - xm] ? rs.blk_f[m - xm][tr] : p.num_valid);
+          fr[i] = __builtin_amdgcn_readfirstlane(tr < rs.blk_n[m - xm] ? rs.blk_f[m - xm][tr] : nv);
         }
       } else {
         sload_block(p.eids, m - xm, p.sti, (m - xm) * 16 + wvu * 4, e, fr);
       }
     }
-    const uint16_t* wbase = extra ? p.Wx : p.W + (int64_t)e * p.swe;
+    if constexpr (PACKED) {
+      // item n of the layout block: load slot ps of packed tile P (gated: half hs of the
+      // `gate` slot and the same half of its `up` slot, four slots on, 512 B each); wave
+      // instruction i loads 32-k stage 16 s + 4 wv + i of the slot(s) for 512-k stage s, so
+      // an item streams its slot's K / 32 KB as one contiguous run
+      const int n = L % num_n;
+      const int P = n >> 5, q5 = n & 31;
+      const int ps = GATED ? (q5 >> 3) * 8 + ((q5 >> 1) & 3) : q5;
+      const uint16_t* tb = uniform_ptr(extra ? pw_x : pw_r) +
+                           ((int64_t)e * num_n512 + P) * packed_tile_elems(nk32) +
+                           ps * packed_slot_elems(nk32);
+      dw[0] = tb + (int64_t)(wvu * 4) * 512;  // the slot's 32-k stages follow 1 KB apart
+      if (GATED) {
+        const int hs = q5 & 1;
+        wvo = (uint32_t)(lane < 32 ? (hs * 32 + lane) * 16
+                                   : 4 * packed_slot_elems(nk32) * 2 + (hs * 32 + lane - 32) * 16);
+      } else {
+        wvo = (uint32_t)(lane * 16);
+      }
+    } else {
+      const uint16_t* wbase = extra ? p.Wx : p.W + (int64_t)e * p.swe;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int row = wvu * 4 + i;  // W tile row
-      const int grow = GATED ? (row < 8 ? n0 + row : p.gu_off + n0 + row - 8) : n0 + row;
-      dw[i] = wbase + (int64_t)grow * p.swn;
+      for (int i = 0; i < 4; ++i) {
+        const int row = wvu * 4 + i;  // W tile row
+        const int grow = GATED ? (row < 8 ? n0 + row : p.gu_off + n0 + row - 8) : n0 + row;
+        dw[i] = wbase + (int64_t)grow * p.swn;
+      }
     }
     da_n = 0;
     int fs[4];
@@ -240,7 +280,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
         da[i] = p.Ax + (int64_t)(ok ? f : 0) * p.sax;
       } else {
         f = fr[i];
-        ok = f < p.num_valid;
+        ok = f < nv;
         da[i] = p.A + (int64_t)(ok ? f / p.a_div : 0) * p.sam;
       }
       da_n += ok ? 1 : 0;
@@ -267,13 +307,21 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int R = wvu * 4 + i;
-      dma16s_nt(dw[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
+      if constexpr (PACKED)
+        dma16s_nt(uniform_ptr(dw[0] + (int64_t)(s * 16 + i) * 512), wvo,
+                  sb + (uint32_t)(R * KS * 2));
+      else
+        dma16s_nt(dw[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int R = 16 + wvu * 4 + i;
-      if (i < da_n)
-        dma16s(da[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
+      if (i < da_n) {
+        if constexpr (PACKED)  // a per-lane address: SGPRs are short in these instances
+          dma16(da[i] + s * KS + (lane ^ (R & 15)) * 8, sb + (uint32_t)(R * KS * 2));
+        else
+          dma16s(da[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
+      }
     }
     return 4 + da_n;  // loads issued
   };
@@ -442,12 +490,28 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   };
 
   // ---- multiply side ------------------------------------------------------------------
-  auto compute = [&](int buf, floatx4_t acc) {
+  // Packed: the W part of a stage holds 16 slabs of 1 KB, slab j the 32-k stage j as the
+  // load wrote it; MFMA row r16 is packed row p = r16 (gated: rows 0-7 the `gate` half,
+  // 8-15 the `up` half, p = 8 hs + r16 % 8 of each slot), and its 8-k chunk g sits in the
+  // lane slot 4 p + (g ^ (p / 4 % 4)).  The element offset of lane (r16, g) in a slab:
+  auto w_ofs = [&](int it) {
+    if constexpr (!PACKED) {
+      return 0;
+    } else if constexpr (GATED) {
+      const int hs = place(it) & 1;  // num_n is even
+      const int pp = r16 & 7;
+      return (r16 >> 3) * 256 + (4 * pp + (g ^ (2 * hs + (pp >> 2)))) * 8;
+    } else {
+      return (4 * r16 + (g ^ ((r16 >> 2) & 3))) * 8;
+    }
+  };
+  auto compute = [&](int buf, floatx4_t acc, int wofs) {
     const uint16_t* sb = ring + buf * SELEM;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = (wv * 4 + q) * 4 + g;  // logical 16-byte chunk of the 512-k run
-      const uint4 wf = *reinterpret_cast<const uint4*>(sb + r16 * KS + ((c ^ r16) * 8));
+      const uint4 wf = PACKED ? *reinterpret_cast<const uint4*>(sb + (wv * 4 + q) * 512 + wofs)
+                              : *reinterpret_cast<const uint4*>(sb + r16 * KS + ((c ^ r16) * 8));
       const uint4 af = *reinterpret_cast<const uint4*>(sb + (16 + r16) * KS + ((c ^ r16) * 8));
       acc = mfma16(wf, af, acc);  // C[W row 4 g + i][token r16]
     }
@@ -467,10 +531,25 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     const int i = row % 4, l = (row / 4) * 16 + c;
     return ((red[par][0][i][l] + red[par][1][i][l]) + red[par][2][i][l]) + red[par][3][i][l];
   };
+  // output column of output j of item L: n0 + j, or packed, row phi32(p) of the slot's
+  // 32-row group (gated p = 8 hs + j)
+  auto out_col = [&](int L, int j) {
+    const int n = L % num_n;
+    if constexpr (!PACKED) {
+      return n * NOC + j;
+    } else if constexpr (GATED) {
+      const int P = n >> 5, q5 = n & 31;
+      const int i = (q5 >> 1) & 3;
+      return P * 256 + (q5 >> 3) * 64 + (i >> 1) * 32 + (i & 1) * 8 + phi32(8 * (q5 & 1) + j);
+    } else {
+      const int P = n >> 5, q5 = n & 31;
+      const int i = q5 & 7;
+      return P * 512 + (q5 >> 3) * 128 + (i >> 1) * 32 + (i & 1) * 8 + phi32(j);
+    }
+  };
   auto finish = [&](int it, int par) {
     const int L = place(it);
     const int m = L / num_n;
-    const int n0 = (L % num_n) * NOC;
     const bool extra = m < xm;
     const int slot = (it / (int)gridDim.x) % NMETA;
     const int c = wv * 4 + lane / 16;  // token column of the slice
@@ -481,7 +560,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       if (WEIGHTED && !extra) v = v * meta_w[slot][c];
       const float v1 = __shfl_down(v, 1, 16);  // every lane is active here
       if (tok < 0 || (j & 1) || extra) return;
-      atomic_add_bf16x2(p.C + (int64_t)(tok / p.merge_topk) * p.scm + n0 + j, v, v1);
+      atomic_add_bf16x2(p.C + (int64_t)(tok / p.merge_topk) * p.scm + out_col(L, j), v, v1);
       return;
     }
     if (GATED && j >= 8) return;
@@ -495,7 +574,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       if (WEIGHTED && !extra) v = v * meta_w[slot][c];
     }
     uint16_t* dst = extra ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm;
-    dst[n0 + j] = f32_to_bf16(v);
+    dst[out_col(L, j)] = f32_to_bf16(v);
   };
 
   // prologue: the first three stages.  In routing mode the logits are loaded first and a
@@ -548,6 +627,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 
   floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
   int c_item = blockIdx.x, c_s = 0;
+  int wofs = w_ofs(c_item);
   int pend = -1, par = 0;  // the item whose partial sums wait in red[par ^ 1], if any
 #pragma unroll 1
   for (int j = 0; j < total; ++j) {
@@ -562,7 +642,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       finish(pend, par ^ 1);
       pend = -1;
     }
-    acc = compute(j % NSTAGE, acc);
+    acc = compute(j % NSTAGE, acc, wofs);
     if (++c_s == nks) {
       stash(par, acc);
       pend = c_item;
@@ -570,6 +650,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       acc = floatx4_t{0.f, 0.f, 0.f, 0.f};
       c_s = 0;
       c_item += gridDim.x;
+      wofs = w_ofs(c_item);
     }
   }
   if (pend >= 0) {
@@ -579,10 +660,14 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   GLM52_WAIT_VMCNT(0);  // the re-reads past the last stage land before the workgroup ends
 }
 
-template <bool GATED, bool WEIGHTED, bool ROUTE>
+template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED>
 int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
   constexpr int NOC = GATED ? 8 : 16;
   if (a.BM != 16 || (a.n_out % NOC) || (a.K % KS) || a.K / KS < 1) return GLM52_EUNSUPPORTED;
+  // packed: whole 512-row tiles (256 outputs gated), no atomic merge
+  if (PACKED && ((a.n_out % (GATED ? 256 : 512)) || a.merge_topk > 0 ||
+                 (a.x_rows > 0 && !a.Wx)))
+    return GLM52_EUNSUPPORTED;
   if (ROUTE && (a.x_rows < 1 || a.r_T < 1 || a.r_T > RT || a.r_topk < 1 || a.r_topk > 8 ||
                 a.r_E < a.r_topk || a.r_E > kMaxE || (a.r_E % 4) ||
                 a.r_capacity < a.r_T * a.r_topk + a.r_E * 15 || (a.r_capacity % 16)))
@@ -590,7 +675,7 @@ int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
   const int items_max = (capacity / 16 + (a.x_rows + 15) / 16) * (a.n_out / NOC);
   int grid = items_max < 256 ? items_max : 256;
   if (grid < 1) grid = 1;
-  moe_gemm_runs_kernel<GATED, WEIGHTED, ROUTE><<<grid, 256, 0, st>>>(a);
+  moe_gemm_runs_kernel<GATED, WEIGHTED, ROUTE, PACKED><<<grid, 256, 0, st>>>(a);
   GLM52_RETURN_LAUNCH();
 }
 
@@ -599,11 +684,19 @@ int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
 namespace glm52 {
 int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, bool route,
                 hipStream_t st) {
+  if (a.Wp) {  // packed weights (glm52_pack_w512)
+    if (route) {
+      if (!gated || weighted) return GLM52_EUNSUPPORTED;
+      return launch_runs_t<true, false, true, true>(a, capacity, st);
+    }
+    if (gated) return weighted ? launch_runs_t<true, true, false, true>(a, capacity, st) : launch_runs_t<true, false, false, true>(a, capacity, st);
+    return weighted ? launch_runs_t<false, true, false, true>(a, capacity, st) : launch_runs_t<false, false, false, true>(a, capacity, st);
+  }
   if (route) {
     if (!gated || weighted) return GLM52_EUNSUPPORTED;
-    return launch_runs_t<true, false, true>(a, capacity, st);
+    return launch_runs_t<true, false, true, false>(a, capacity, st);
   }
-  if (gated) return weighted ? launch_runs_t<true, true, false>(a, capacity, st) : launch_runs_t<true, false, false>(a, capacity, st);
-  return weighted ? launch_runs_t<false, true, false>(a, capacity, st) : launch_runs_t<false, false, false>(a, capacity, st);
+  if (gated) return weighted ? launch_runs_t<true, true, false, false>(a, capacity, st) : launch_runs_t<true, false, false, false>(a, capacity, st);
+  return weighted ? launch_runs_t<false, true, false, false>(a, capacity, st) : launch_runs_t<false, false, false, false>(a, capacity, st);
 }
 }  // namespace glm52

@@ -329,14 +329,12 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 // ------------------------------------------------------------------------------------
 namespace {
 
-// W row (inside its 32-row group) held at LDS row p.
-GLM52_DEV int phi32(int p) { return ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); }
-
-// Packed W (PACKED): for expert e and output tile pid_n the tile's stages follow each other,
-// 32 KB each ((e * num_n + pid_n) * nk + kt), and inside a stage the 1 KB of wave w's load
-// instruction i sits at (w * 8 + i) * 1 KB, lane l's 16 bytes at l * 16: exactly what the
-// instruction writes to LDS, so every load reads 1 KB of contiguous memory.
-constexpr int kPackStage = 32768;  // bytes of one packed stage (512 rows x 32 k x 2 B)
+// Packed W (PACKED): expert e's 512-row tiles P follow each other; inside a tile its 32 load
+// slots (slot w * 8 + i: what load instruction i of wave w fetches), nk KB each; inside a
+// slot its nk stages, 1 KB each, lane l's 16 bytes at l * 16: exactly
+// what the instruction writes to LDS.  Every load reads 1 KB of contiguous memory, and a
+// slot's successive stages are adjacent, which the decode weight stream (one slot per item)
+// reads as one contiguous run.
 
 // W row (relative to the tile's first `gate` row, or to n0) and k chunk of packed lane l of
 // load instruction i of wave w: the row and chunk the unpacked loads of that slot fetch.
@@ -462,14 +460,15 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     // tile: packed, 1 KB of contiguous memory; in place, W rows wrow + phi32(lane / 4), 16
     // bytes at logical chunk dc each (the lane's byte offsets inside W[e], < 2^32)
     const uint16_t* wexp = PACKED ? (xs ? p.Wx : p.Wp) +
-                                        ((int64_t)(e * num_n512 + P) * nk * SPLIT + sub) *
-                                            (kPackStage / 2 / SPLIT)
+                                        (int64_t)(e * num_n512 + P) * packed_tile_elems(nk)
                                   : p.W + (int64_t)e * p.swe;
     uint32_t wvoff[WI];
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
       if (PACKED) {
-        wvoff[i] = (uint32_t)((wv * WI + i) * 1024 + lane * 16);
+        // load slot sub * 32 / SPLIT + wv * WI + i of the 512-row tile: nk KB per slot
+        wvoff[i] = (uint32_t)((sub * (32 / SPLIT) + wv * WI + i) * packed_slot_elems(nk) * 2 +
+                              lane * 16);
       } else {
         const int slab = sub * (NTW / RPI) + wv * WI + i;  // 1 KB slab of the 512-row tile
         const int row = P * NO512 + w512_row(GATED, p.gu_off, slab / 8, slab % 8, lane);
@@ -492,7 +491,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       const int kc = min(kt, nk - 1) * BKS;
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
-        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * (kPackStage / 2) : wexp + kc;
+        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * 512 : wexp + kc;
         const uint32_t vo = past ? 0u : wvoff[i];
         if (w_once)
           dma16s_nt(src, vo, sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
@@ -719,8 +718,9 @@ int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
   }
 }
 
-// One 16-byte chunk of the packed layout per thread and step: destination chunk d is lane
-// d % 64 of load instruction (d / 64) % 32 of stage (d / 2048) % nk of tile d / (2048 nk).
+// One 16-byte chunk of the packed layout per thread and step: chunk d is lane d % 64 of
+// stage (d / 64) % nk of load slot (d / (64 nk)) % 32 of tile d / (2048 nk), written at
+// stage KB (+ 16 lane bytes) of that slot, the slots nk KB apart.
 template <bool GATED>
 __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restrict__ w,
                                                         int64_t swe, int64_t swn, int64_t swk,
@@ -731,17 +731,19 @@ __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restri
   for (int64_t d = (int64_t)blockIdx.x * 256 + threadIdx.x; d < chunks;
        d += (int64_t)gridDim.x * 256) {
     const int l = (int)(d % 64);
-    const int slot = (int)((d / 64) % 32);
-    const int64_t rest = d / 2048;
-    const int kt = (int)(rest % nk);
-    const int64_t tile = rest / nk;
+    const int64_t q = d / 64;
+    const int kt = (int)(q % nk);
+    const int64_t rest = q / nk;  // tile * 32 + slot
+    const int slot = (int)(rest % 32);
+    const int64_t tile = rest / 32;
+    uint16_t* dst = out + rest * packed_slot_elems(nk) + kt * 512 + l * 8;
     const int pid_n = (int)(tile % num_n);
     const int64_t e = tile / num_n;
     const int row = pid_n * NO + w512_row(GATED, gu_off, slot / 8, slot % 8, l);
     const int64_t k0 = (int64_t)kt * 32 + w512_chunk(l) * 8;
     const uint16_t* src = w + e * swe + (int64_t)row * swn + k0 * swk;
     if (swk == 1) {
-      *reinterpret_cast<uint4*>(out + d * 8) = *reinterpret_cast<const uint4*>(src);
+      *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(src);
     } else {  // k strided (a [K, N] operand packed as its transpose): gather 8 values
       uint16_t v[8];
 #pragma unroll
@@ -751,7 +753,7 @@ __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restri
       o.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
       o.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
       o.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
-      *reinterpret_cast<uint4*>(out + d * 8) = o;
+      *reinterpret_cast<uint4*>(dst) = o;
     }
   }
 }
@@ -770,8 +772,8 @@ int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_o
   const int NO = gated ? 256 : 512;
   if (E <= 0 || n_out <= 0 || (n_out % NO) || k <= 0 || (k % 64)) return GLM52_EUNSUPPORTED;
   const int num_n = n_out / NO, nk = k / 32;
-  const int64_t chunks = (int64_t)E * num_n * nk * 2048;
-  const int64_t bytes = chunks * 16;
+  const int64_t chunks = (int64_t)E * num_n * nk * 2048;  // 16-byte chunks written
+  const int64_t bytes = (int64_t)E * num_n * packed_tile_elems(nk) * 2;
   if (!out) return bytes;
   const int64_t blocks = (chunks + 255) / 256;
   const int grid = (int)(blocks < 65536 ? blocks : 65536);

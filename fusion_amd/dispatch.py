@@ -169,3 +169,35 @@ def route_gateup_shared_into(logits, cfg, topw, topi, sorted_token_ids, expert_i
         act.stride(0), _lib.ptr(a_shared), a_shared.stride(0), _lib.ptr(ws), _lib.ptr(act_shared),
         act_shared.stride(0), I, a.shape[1], _lib.stream(),
     )
+
+
+def route_gateup_shared_packed_into(logits, cfg, topw, topi, sorted_token_ids, expert_ids,
+                                    num_tokens_post_padded, a, w13_packed, act, a_shared,
+                                    w13_shared_packed, act_shared):
+    """`route_gateup_shared_into` on packed weights (`pack_w512(w13, I, I, True)` and the
+    same of the [1, 2I, H] shared w13): the same routing, layout and bits."""
+    from .kernels.moe_gateup import check_packed
+    bias = cfg.get("correction_bias")
+    _lib.require_gpu(logits, topw, topi, bias, sorted_token_ids, expert_ids,
+                     num_tokens_post_padded, a, w13_packed, act, a_shared, w13_shared_packed,
+                     act_shared)
+    T, E = logits.shape
+    k = topi.shape[1]
+    for t, n in ((a, "a"), (w13_packed, "w13_packed"), (act, "act"), (a_shared, "a_shared"),
+                 (w13_shared_packed, "w13_shared_packed"), (act_shared, "act_shared")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be bf16 and contiguous along its last dim")
+    I, H = act.shape[1], a.shape[1]
+    check_packed(w13_packed, I, H, True)
+    check_packed(w13_shared_packed, I, H, True)
+    if w13_packed.numel() * 2 < E * _lib.query("glm52_packed_w512_bytes", 1, I, H, 1):
+        raise ValueError(f"w13_packed holds fewer than the router's {E} experts")
+    _lib.call(
+        "glm52_moe_gemm_route_shared_packed", _lib.ptr(logits), logits.stride(0), _lib.ptr(bias),
+        T, E, k, float(cfg.get("scale", 2.5)), int(bool(cfg.get("NORM_PROB", True))),
+        _lib.ptr(topw), topw.stride(0), _lib.ptr(topi), topi.stride(0),
+        _lib.ptr(sorted_token_ids), _lib.ptr(expert_ids), _lib.ptr(num_tokens_post_padded),
+        sorted_token_ids.numel(), _lib.ptr(a), a.stride(0), _lib.ptr(w13_packed), _lib.ptr(act),
+        act.stride(0), _lib.ptr(a_shared), a_shared.stride(0), _lib.ptr(w13_shared_packed),
+        _lib.ptr(act_shared), act_shared.stride(0), I, H, _lib.stream(),
+    )

@@ -115,6 +115,49 @@ def launch_down_token_major(a, w2, out, topk_weights, topk_ids, residual, top_k,
     )
 
 
+def launch_down_token_major_packed(a, w2_packed, out, topk_weights, topk_ids, residual, top_k,
+                                   add_residual: bool, a_shared=None, w2_shared_packed=None):
+    """`launch_down_token_major` on packed weights (`pack_w512(w2, H, 0, False)` and, for the
+    shared expert, the same of its [1, H, I] w2): the same sum, one fp32 accumulation and
+    one rounding, with the adds in another order.  out: [T, H]; a: [T*top_k, I]."""
+    from .moe_gateup import check_packed
+    _lib.require_gpu(a, w2_packed, out, topk_weights, topk_ids,
+                     residual if add_residual else None, a_shared, w2_shared_packed)
+    T = topk_ids.shape[0]
+    H, K = out.shape[1], a.shape[1]
+    for t, n in ((a, "a"), (w2_packed, "w2_packed"), (out, "out")):
+        if t.dtype != torch.bfloat16 or t.stride(-1) != 1:
+            raise ValueError(f"{n} must be bf16 and contiguous along its last dim")
+    if a.shape[0] < T * top_k or out.shape[0] != T:
+        raise ValueError(f"shape mismatch: a {tuple(a.shape)}, out {tuple(out.shape)}, "
+                         f"T={T}, top_k={top_k}")
+    check_packed(w2_packed, H, K, False)
+    E = w2_packed.numel() * 2 // _lib.query("glm52_packed_w512_bytes", 1, H, K, 0)
+    if topk_ids.dtype != torch.int32:
+        topk_ids = topk_ids.to(torch.int32)
+    if topk_weights.dtype != torch.float32 or topk_weights.stride(1) != 1 \
+            or topk_ids.stride(1) != 1 or topk_ids.stride(0) != topk_weights.stride(0):
+        raise ValueError("topk weights (fp32) and ids (int32) must share a row stride")
+    res = residual if add_residual else None
+    if res is not None and (tuple(res.shape) != (T, H) or res.stride(1) != 1):
+        raise ValueError("residual must be [T, H] with H contiguous")
+    if (a_shared is None) != (w2_shared_packed is None):
+        raise ValueError("a_shared and w2_shared_packed go together")
+    if w2_shared_packed is not None:
+        check_packed(w2_shared_packed, H, K, False)
+        if w2_shared_packed.numel() * 2 != _lib.query("glm52_packed_w512_bytes", 1, H, K, 0):
+            raise ValueError("w2_shared_packed must hold one expert")
+        if a_shared.shape[-1] != K or a_shared.stride(-1) != 1:
+            raise ValueError("a_shared must be [T, I] with I contiguous")
+    _lib.call(
+        "glm52_down_token_major_packed", _lib.ptr(a), a.stride(0), _lib.ptr(w2_packed),
+        _lib.ptr(topk_weights), _lib.ptr(topk_ids), topk_ids.stride(0), int(top_k), E,
+        _lib.ptr(a_shared), a_shared.stride(0) if a_shared is not None else 0,
+        _lib.ptr(w2_shared_packed), _lib.ptr(res), res.stride(0) if res is not None else 0,
+        _lib.ptr(out), out.stride(0), T, H, K, _lib.stream(),
+    )
+
+
 def launch_moe_sum(c3, out, residual, topk, cfg, add_residual: bool):
     """c3: [T, topk, H] (or a [rows, H] view).  out: [T, H]."""
     _lib.require_gpu(c3, out, residual if add_residual else None)

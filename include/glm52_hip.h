@@ -163,6 +163,25 @@ int glm52_moe_gemm_route_shared(const float* logits, int64_t stride_l, const flo
                                 void* c_shared, int64_t stride_cs, int n_out, int k,
                                 hipStream_t stream);
 
+/* glm52_moe_gemm_route_shared on packed weights: w_packed = glm52_pack_w512 of w13 (gated,
+ * n_out outputs, gate_up_offset n_out), w_shared_packed the same of the [1, 2 n_out, k]
+ * shared w13; n_out % 256 == 0, k % 512 == 0.  The same routing, layout and bits as the
+ * row-major entry.  Replaces the same reference chain: norm_router.topk_only
+ * (glm52/kernels/norm_router.py:352-354) -> reference.moe_align_block_size
+ * (glm52/reference.py:85-128) -> moe_gateup.launch_gateup(fused=True)
+ * (glm52/kernels/moe_gateup.py:199-248), routed and shared (glm52/bench/bench_layer.py:470-480),
+ * on the one resident weight layout this build keeps. */
+int glm52_moe_gemm_route_shared_packed(const float* logits, int64_t stride_l, const float* bias,
+                                       int T, int E, int topk, float scale, int norm_prob,
+                                       float* topw, int64_t stride_w, int32_t* topi,
+                                       int64_t stride_i, int32_t* sorted_token_ids,
+                                       int32_t* expert_ids, int32_t* num_tokens_post_padded,
+                                       int capacity, const void* a, int64_t stride_am,
+                                       const void* w_packed, void* c, int64_t stride_cm,
+                                       const void* a_shared, int64_t stride_as,
+                                       const void* w_shared_packed, void* c_shared,
+                                       int64_t stride_cs, int n_out, int k, hipStream_t stream);
+
 /* Grouped expert GEMM on bf16 MFMA.  Replaces moe_gateup.launch_gateup
  * (glm52/kernels/moe_gateup.py:199-248; gated = fused SwiGLU, gate_up_offset = I) and
  * moe_down_merge.launch_down with fuse_merge=False (glm52/kernels/moe_down_merge.py:427-476;
@@ -194,17 +213,20 @@ int glm52_moe_gemm_shared(const void* a, int64_t stride_am, int a_row_div, const
                           const void* w_shared, void* c_shared, int64_t stride_cs,
                           int shared_rows, int n_out, int k, int gated, hipStream_t stream);
 
-/* Packed weights for the prefill mapping (block_m 64 or 128): no counterpart in the
- * reference, whose kernels read W in place.  That mapping reads each 32-k stage of a
+/* Packed weights, the one resident layout of this build's block: no counterpart in the
+ * reference, whose kernels read W in place.  The prefill mapping reads each 32-k stage of a
  * 512-row W tile as 512 runs of 64 bytes; the packed copy holds every stage as 32 KB of
- * contiguous memory in the order the tile's loads fill LDS.  Packing is done once per
- * weight tensor; the GEMM on the packed copy computes the same bits as glm52_moe_gemm
- * (variant 5) on the original.
+ * contiguous memory in the order the tile's loads fill LDS, and each 1 KB load slot of a
+ * stage (16 rows x 32 k) is also what the decode weight stream reads.  Packing is done once
+ * per weight tensor; the GEMMs on the packed copy compute the same bits as glm52_moe_gemm
+ * (variants 5 and 6) on the original.
  *   glm52_packed_w512_bytes: bytes of the packed copy of num_experts experts' W for n_out
  *     outputs (gated: `gate` rows n and `up` rows gate_up_offset + n) and K = k; negative
  *     if the mapping has no instance for the shape (n_out % 256 gated / 512 plain, k % 64).
  *   glm52_pack_w512: writes that copy (w, strides, gate_up_offset as for glm52_moe_gemm).
- *   glm52_moe_gemm_packed: glm52_moe_gemm with block_m 64 or 128 on the packed copy. */
+ *   glm52_moe_gemm_packed: glm52_moe_gemm with block_m 64, 128 or 256 on the packed copy,
+ *     or with block_m 16 (the decode weight stream, k % 512 == 0), which reads each packed
+ *     load slot -- 16 rows x 32 k, 1 KB of contiguous memory -- as it streams the rows. */
 int64_t glm52_packed_w512_bytes(int num_experts, int n_out, int k, int gated);
 int glm52_pack_w512(const void* w, int64_t stride_we, int64_t stride_wn, int num_experts,
                     int n_out, int k, int gate_up_offset, int gated, void* packed,
@@ -307,6 +329,20 @@ int glm52_down_token_major(const void* a, int64_t stride_am, const void* w2, int
                            int64_t stride_as, const void* w2_shared, int64_t stride_ws,
                            const void* residual, int64_t stride_rm, void* out, int64_t stride_om,
                            int T, int N, int K, hipStream_t stream);
+
+/* glm52_down_token_major on packed weights: w2_packed = glm52_pack_w512 of w2 ([E, N, K],
+ * plain, n_out = N), w2_shared_packed (may be null) the same of the [1, N, K] shared w2;
+ * N % 512 == 0, K 1024 or 2048, a / a_shared row strides as for glm52_down_token_major.
+ * The same sum with one fp32 accumulation and one rounding, its adds in another order.
+ * Replaces moe_down_merge.launch_down_token_major (glm52/kernels/moe_down_merge.py:479-516)
+ * on the one resident weight layout this build keeps. */
+int glm52_down_token_major_packed(const void* a, int64_t stride_am, const void* w2_packed,
+                                  const float* topk_weights, const int32_t* topk_ids,
+                                  int64_t stride_tk, int top_k, int num_experts,
+                                  const void* a_shared, int64_t stride_as,
+                                  const void* w2_shared_packed, const void* residual,
+                                  int64_t stride_rm, void* out, int64_t stride_om, int T, int N,
+                                  int K, hipStream_t stream);
 
 /* y[M, I] = bf16(silu(x[:, :I]) * x[:, I:]).  Replaces moe_gateup.launch_silu_and_mul
  * (glm52/kernels/moe_gateup.py:251-266). */

@@ -530,6 +530,64 @@ def test_packed_w512_matches_unpacked(gpu, bm, T, E, H, I):
     _close(act, _gateup_ref(a, w13, ids, k, I, True), "w13 (packed path reference)")
 
 
+@pytest.mark.parametrize("T", [1, 3, 16, 40])
+def test_packed_weight_stream_matches_in_place(gpu, T):
+    """The decode weight stream (block size 16) on packed weights, routed and shared expert
+    in one launch: the same bits as on the weights in place -- gated w13 + SwiGLU, weighted
+    w2 -- and the packed token-major tail within one bf16 rounding step of the in-place one
+    (it adds in another order; 1e-3 absolute where the sum cancels) and both within bf16
+    rounding of the fp32 reference."""
+    E, H, I, k = 8, 1024, 1024, 8
+    say(f"packed weight stream T={T} E={E} H={H} I={I}")
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 90 + T, gpu)
+    ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
+    g = torch.Generator().manual_seed(5)
+    w13s = (torch.randn(1, 2 * I, H, generator=g) * 0.02).to(BF16).to(gpu)
+    w2s = (torch.randn(1, H, I, generator=g) * 0.02).to(BF16).to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), 16, E)
+    cfg = {"BLOCK_M": 16}
+    R = T * k
+    w13p, w2p = KG.pack_w512(w13g, I, I, True), KG.pack_w512(w2g, H, 0, False)
+    w13sp, w2sp = KG.pack_w512(w13s, I, I, True), KG.pack_w512(w2s, H, 0, False)
+    act = torch.empty(R, I, dtype=BF16, device=gpu)
+    act_s = torch.empty(T, I, dtype=BF16, device=gpu)
+    KG.moe_gemm_shared(ag, k, w13g, act, None, sti, eids, ntp, R, I, I, True, cfg, ag, w13s,
+                       act_s)
+    act_p, act_sp = torch.full_like(act, float("nan")), torch.full_like(act_s, float("nan"))
+    KG.moe_gemm_packed_shared(ag, k, w13p, act_p, None, sti, eids, ntp, R, I, True, cfg, ag,
+                              w13sp, act_sp)
+    twf = tw.reshape(-1).contiguous().to(gpu)
+    y = torch.empty(R, H, dtype=BF16, device=gpu)
+    s_out = torch.empty(T, H, dtype=BF16, device=gpu)
+    KG.moe_gemm_shared(act, 1, w2g, y, twf, sti, eids, ntp, R, H, 0, False, cfg, act_s, w2s,
+                       s_out)
+    y_p, s_p = torch.full_like(y, float("nan")), torch.full_like(s_out, float("nan"))
+    KG.moe_gemm_packed_shared(act, 1, w2p, y_p, twf, sti, eids, ntp, R, H, False, cfg, act_s,
+                              w2sp, s_p)
+    # the token-major tail, both layouts, + a residual
+    h = (torch.randn(T, H, generator=g) * 0.5).to(BF16).to(gpu)
+    twg, idg = tw.to(gpu).float().contiguous(), ids.to(gpu).int().contiguous()
+    out = torch.empty(T, H, dtype=BF16, device=gpu)
+    KD.launch_down_token_major(act, w2g, out, twg, idg, h, k, {}, True, act_s, w2s)
+    out_p = torch.full_like(out, float("nan"))
+    KD.launch_down_token_major_packed(act, w2p, out_p, twg, idg, h, k, True, act_s, w2sp)
+    torch.cuda.synchronize()
+    assert torch.equal(act_p, act)
+    assert torch.equal(act_sp, act_s)
+    assert torch.equal(y_p, y)
+    assert torch.equal(s_p, s_out)
+    # one bf16 rounding step apart, plus the fp32 reordering where the sum cancels
+    d = (out_p.float() - out.float()).abs()
+    assert (d <= torch.maximum(out_p.float().abs(), out.float().abs()) * 2.0 ** -7 + 1e-3).all()
+    ref = h.float() + act_s.float() @ w2s[0].float().t()
+    for t in range(T):
+        for j in range(k):
+            ref[t] += twg[t, j] * (act[t * k + j].float() @ w2g[idg[t, j]].float().t())
+    _close(out_p, ref.cpu(), "token-major tail on packed weights")
+    _close(out, ref.cpu(), "token-major tail in place")
+    _close(act, _gateup_ref(a, w13, ids, k, I, True), "w13 (weight stream reference)")
+
+
 def test_pack_w512_rejects_unsupported_shape(gpu):
     w = torch.zeros(2, 384, 512, dtype=BF16, device=gpu)
     with pytest.raises(ValueError, match="no 512-row tile instance"):

@@ -10,7 +10,9 @@ resident, at the token counts of the benchmark configurations.
   fp32 ground truth, and within the reference's own `rel_err <= 2e-2` gate
   (`glm52/common.py:186-200`) of its framework-faithful path
   (`glm52/bench/bench_layer.py:365-374`);
-* HIP-graph replay and repeat launches: bitwise identical to the eager result.
+* HIP-graph replay and repeat launches: bitwise identical to the eager result;
+* the one resident layout: the block on packed weights (`PackedExperts`) against the block
+  reading the row-major weights in place, at the decode sizes whose mappings differ.
 """
 
 from __future__ import annotations
@@ -23,7 +25,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from fusion_amd.block import MoEBlock
+from fusion_amd.block import MoEBlock, PackedExperts
 from fusion_amd.problem import expert_weights, front_end
 from oracle import glm52_oracle as O
 
@@ -45,6 +47,16 @@ def weights(gpu):
     torch.cuda.synchronize()
     yield w
     del w
+    torch.cuda.empty_cache()
+
+
+@pytest.fixture(scope="module")
+def packed(weights):
+    say("packing the weight set (the block's one resident layout)")
+    p = PackedExperts(weights.w13, weights.w2, weights.w13s, weights.w2s)
+    torch.cuda.synchronize()
+    yield p
+    del p
     torch.cuda.empty_cache()
 
 
@@ -144,12 +156,12 @@ CONFIGS = [(1, "normal"), (4, "zipf"), (16, "normal"), (32, "normal"), (256, "no
 
 
 @pytest.mark.parametrize("T,bias", CONFIGS)
-def test_block_parity(gpu, weights, T, bias):
+def test_block_parity(gpu, weights, packed, T, bias):
     say(f"block T={T} bias={bias}")
     fe = front_end(T, bias=bias)
     x, r = fe.x.to(gpu), fe.r.to(gpu)
-    blk = MoEBlock(T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu), weights.w13,
-                   weights.w2, weights.w13s, weights.w2s)
+    blk = MoEBlock(T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu), packed)
+    assert blk.packed and blk.w13 is None  # one layout held
     out = blk(x, r).clone()
     torch.cuda.synchronize()
 
@@ -204,12 +216,11 @@ def test_block_parity(gpu, weights, T, bias):
 
 
 @pytest.mark.parametrize("T", [1, 256, 2048])
-def test_block_graph_replay(gpu, weights, T):
+def test_block_graph_replay(gpu, packed, T):
     say(f"graph replay T={T}")
     fe = front_end(T)
     x, r = fe.x.to(gpu), fe.r.to(gpu)
-    blk = MoEBlock(T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu), weights.w13,
-                   weights.w2, weights.w13s, weights.w2s)
+    blk = MoEBlock(T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu), packed)
     eager = blk(x, r).clone()
     blk.capture(x, r)
     for i in range(3):
@@ -220,6 +231,42 @@ def test_block_graph_replay(gpu, weights, T):
         torch.cuda.synchronize()
         assert torch.equal(got, eager), f"replay {i} differs from eager"
         _ = (x.float() * 2).sum().item()  # eager work between replays
+
+
+@pytest.mark.parametrize("T,bias", [(1, "normal"), (4, "zipf"), (16, "normal"),
+                                    (256, "normal")])
+def test_block_layouts_agree(gpu, weights, packed, T, bias):
+    """The decode mappings on the packed layout (the routing w13 launch, the weight stream
+    at block size 16, the token-major tail) against the same mappings reading the row-major
+    weights in place: the GEMM outputs bit for bit; the token-major tail, which adds in
+    another order, to one bf16 rounding step (1e-3 absolute where the sum cancels; both
+    tails also meet the block parity test's fp32 ground truth)."""
+    say(f"packed vs row-major layout T={T} bias={bias}")
+    fe = front_end(T, bias=bias)
+    x, r = fe.x.to(gpu), fe.r.to(gpu)
+    args = (T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu))
+    bp = MoEBlock(*args, packed)
+    br = MoEBlock(*args, weights.w13, weights.w2, weights.w13s, weights.w2s, pack=False)
+    assert bp.packed and not br.packed and bp.token_major == br.token_major
+    op = bp(x, r).clone()
+    orr = br(x, r).clone()
+    torch.cuda.synchronize()
+    for name in ("topi", "topw", "sti", "eids", "ntp", "act_s"):
+        assert torch.equal(getattr(bp, name), getattr(br, name)), name
+    R = T * bp.topk
+    valid = bp.sti[: int(bp.ntp.item())]
+    rows = valid[valid < R].long()
+    assert torch.equal(bp.act[rows], br.act[rows])
+    if bp.token_major:
+        # one bf16 rounding step apart, plus the fp32 reordering where the sum cancels
+        d = (op.float() - orr.float()).abs()
+        ulp = torch.maximum(op.float().abs(), orr.float().abs()) * 2.0 ** -7 + 1e-3
+        assert (d <= ulp).all(), f"max diff {d.max().item()}"
+        say(f"  token-major tail: {int((d > 0).sum())} of {d.numel()} elements one step apart")
+    else:
+        assert torch.equal(bp.ybuf[rows], br.ybuf[rows])
+        assert torch.equal(bp.s_out, br.s_out)
+        assert torch.equal(op, orr)
 
 
 @pytest.fixture
