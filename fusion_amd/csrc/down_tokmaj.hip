@@ -118,10 +118,10 @@ __global__ __launch_bounds__(256) void down_tokmaj_kernel(
 // of packed load slot q of 512-row tile P are rows P * 512 + (q / 8) * 128 + (q % 8 / 2) * 32
 // + (q % 2) * 8 + phi32(p), p = 0 .. 15; the slot holds their K / 32 stages one after the
 // other, 1 KB each, lane l's 16 bytes holding row p = l / 4, 8-k chunk (l % 4) ^ (p / 4 % 4).
-// Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token t: wave w takes stages
-// 2 QS w .. 2 QS w + 2 QS - 1 as two pieces of QS (QS KB of contiguous memory each), every
-// load reads one stage's whole 1 KB, and a lane keeps one fp32 partial of its row over all
-// pieces.  The 4 lanes of a row, then the 4 waves, meet in a fixed order.  The pieces flow
+// Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token t: wave w takes the
+// pieces of QS stages (QS KB of contiguous memory) that start at stages QS w and QS (4 + w),
+// so the four waves read one 4 QS KB run at a time; every load reads one stage's whole 1 KB,
+// and a lane keeps one fp32 partial of its row over all pieces.  The 4 lanes of a row, then the 4 waves, meet in a fixed order.  The pieces flow
 // through two register buffers, so a wave has two pieces' loads in flight; four waves per
 // workgroup let two workgroups share a CU (about 210 VGPRs), so at T = 1 and N = 6144 the
 // 384 workgroups run in a single round.
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
   // token, or (u == topk) the shared expert
   auto load_piece = [&](int c, uint4 (&wr)[QS], uint4 (&ar)[QS], float& wk) {
     const int u = c >> 1;
-    const int kt0 = (2 * wv + (c & 1)) * QS;
+    const int kt0 = ((c & 1) * 4 + wv) * QS;
     const uint16_t* wb = nullptr;
     const uint16_t* arow = nullptr;
     wk = 0.f;
