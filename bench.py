@@ -10,9 +10,14 @@ and 8192 (configurations 2-4, the last with the skewed router bias, whose expert
 are reported with it) are under `per_T`.  Timing follows the reference's `bench_chain`
 (`glm52/common.py:73-122`): one cache flush (1 GiB, larger than the 256 MB Infinity
 Cache) before every step, never inside it, HIP events around the step, eager launches;
-decode sizes also report the replay of a captured HIP graph (`graph_us`).  The dominant kernel -- the block's w13 + SwiGLU
-launch, which at T <= 4 also derives the routing and runs the shared expert -- is also
-timed alone with events on its stream, for the `roofline` object; its HBM traffic comes
+decode sizes also report the replay of a captured HIP graph (`graph_us`).  Each size
+reports the reference's timing record: median, p10, p90, mean and min over the timed
+steps and the median of the same steps without the flush; the headline size also lists
+every step.  The dominant kernel -- the block's w13 + SwiGLU launch, which at T <= 4 also
+derives the routing and runs the shared expert -- is timed with events on its stream
+around it inside whole blocks (after the flush and the front end, before the tail): that
+mean is the `roofline` object's `avg_us`; the same launch timed alone is `solo_us`.  Its
+HBM traffic comes
 from two `rocprofv3 --pmc` runs of a child process (`--pmc-child`), scaled by a plain
 copy of known size.  The CPU baseline is the oracle's restatement of
 `glm52/reference.py`'s path (fp32 router, per-expert bf16 `moe_mlp`, fp32 shared expert)
@@ -123,7 +128,7 @@ def main() -> int:
     def flush():
         flush_buf.zero_()
 
-    def timed(fn, steps, warmup):
+    def timed(fn, steps, warmup, do_flush=True):
         for _ in range(warmup):
             flush()
             fn()
@@ -132,7 +137,8 @@ def main() -> int:
               for _ in range(steps)]
         w0 = time.perf_counter()
         for s, e in ev:
-            flush()
+            if do_flush:
+                flush()
             s.record()
             fn()
             e.record()
@@ -140,6 +146,26 @@ def main() -> int:
         wall = time.perf_counter() - w0
         ms = [s.elapsed_time(e) for s, e in ev]
         return ms, wall
+
+    def timed_inside(before, fn, after, steps, warmup):
+        """Events around `fn` only, inside whole blocks: flush, before(), [fn], after()."""
+        for _ in range(warmup):
+            flush()
+            before()
+            fn()
+            after()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(steps)]
+        for s, e in ev:
+            flush()
+            before()
+            s.record()
+            fn()
+            e.record()
+            after()
+        torch.cuda.synchronize()
+        return [s.elapsed_time(e) for s, e in ev]
 
     tokens = [int(t) for t in args.tokens.split(",") if t]
     per_T = {}
@@ -158,27 +184,37 @@ def main() -> int:
         # sizes also time a captured HIP graph of the same chain (reported, not headline:
         # on this ROCm its replay adds launch gaps between the nodes)
         ms, wall = timed(lambda: blk(x, r), args.steps, args.warmup)
+        # the reference's no-flush median (`glm52/common.py:95-110`), same steps
+        nf_ms, _ = timed(lambda: blk(x, r), args.steps, 2, do_flush=False)
         graph_ms = None
         if (not args.no_graph) and T <= 256:
             blk.capture(x, r)
             graph_ms, _ = timed(blk.replay, args.steps, args.warmup)
 
-        # dominant kernel alone: the block's w13 + SwiGLU launch, events on its stream
-        k_ms, _ = timed(blk.w13_step, args.steps, 2)
+        # dominant kernel: the block's w13 + SwiGLU launch, events on its stream around it
+        # inside whole blocks (the figure the roofline uses), and the same launch alone
+        k_ms = timed_inside(lambda: blk.front_end(x, r), blk.w13_step, blk.tail, args.steps, 2)
+        solo_ms, _ = timed(blk.w13_step, args.steps, 2)
         kc = RL.w13_launch(T, n_e, blk.shared_fused or blk.packed, blk.front_fused)
         k_us = statistics.mean(k_ms) * 1e3
         roof_us = RL.block_roofline_us(T, n_e)
-        med_us = statistics.median(ms) * 1e3
+        st = step_stats(ms)
+        med_us = st["p50_us"]
         rec = {
-            "us_per_block": round(med_us, 2),
-            "us_mean": round(statistics.mean(ms) * 1e3, 2),
-            "us_min": round(min(ms) * 1e3, 2),
+            "us_per_block": med_us,
+            "p10_us": st["p10_us"],
+            "p90_us": st["p90_us"],
+            "us_mean": st["mean_us"],
+            "us_min": st["min_us"],
+            "noflush_p50_us": step_stats(nf_ms)["p50_us"],
             "graph_us": round(statistics.median(graph_ms) * 1e3, 2) if graph_ms else None,
             "wall_us_per_step_incl_flush": round(wall / args.steps * 1e6, 1),
             "distinct_experts": n_e,
             "block_roofline_us": round(roof_us, 1),
             "block_roofline_frac": round(roof_us / med_us, 4),
             "w13_us": round(k_us, 2),
+            "w13_p50_us": step_stats(k_ms)["p50_us"],
+            "w13_solo_us": round(statistics.mean(solo_ms) * 1e3, 2),
             "w13_GBps": round(kc.bytes / (k_us * 1e-6) / 1e9, 1),
             "w13_TFLOPs": round(kc.flops / (k_us * 1e-6) / 1e12, 1),
             "w13_launch": w13_kernel_name(blk),
@@ -194,6 +230,9 @@ def main() -> int:
             rec["down_merge"] = down_merge_bench(blk, W, T, n_e, timed, args.steps, args.warmup)
             rec["oproj"] = oproj_bench(T, timed, args.steps, args.warmup, dev)
             rec["prenorm_router"] = prenorm_bench(T, timed, args.steps, args.warmup, dev)
+        if headline is None:
+            # every timed step of the headline size, in order (µs)
+            rec["step_us"] = [round(v * 1e3, 2) for v in ms]
         per_T[str(T)] = rec
         log(f"T={T}: {rec}")
         if headline is None:
@@ -203,9 +242,12 @@ def main() -> int:
 
     T, rec, kc, k_us, n_e, kname = headline
     achieved = kc.bytes / (k_us * 1e-6) / 1e9
+    # avg_us: the launch's mean duration inside the timed blocks (events around it); the
+    # launch timed alone after a flush is kept beside it as solo_us
     roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": 8000.0, "unit": "GB/s",
             "frac": round(achieved / 8000.0, 4), "traffic": None, "kernel": kname,
-            "algorithmic_bytes": int(kc.bytes), "avg_us": round(k_us, 2)}
+            "algorithmic_bytes": int(kc.bytes), "avg_us": round(k_us, 2),
+            "solo_us": rec["w13_solo_us"]}
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(W, tokens, args.cpu_seconds)
@@ -236,6 +278,16 @@ def main() -> int:
     if args.json_out:
         Path(args.json_out).write_text(s + "\n")
     return 0
+
+
+def step_stats(ms: list) -> dict:
+    """p10 / p50 / p90 / mean / min (µs) of per-step times in ms, with the reference's
+    index rule for the percentiles (`glm52/common.py:112-121`)."""
+    ts = sorted(ms)
+    n = len(ts)
+    return {"p50_us": round(ts[n // 2] * 1e3, 2), "p10_us": round(ts[max(0, int(0.1 * n))] * 1e3, 2),
+            "p90_us": round(ts[min(n - 1, int(0.9 * n))] * 1e3, 2),
+            "mean_us": round(statistics.fmean(ts) * 1e3, 2), "min_us": round(ts[0] * 1e3, 2)}
 
 
 PMC_LAUNCHES = 3
@@ -403,11 +455,14 @@ def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
     (`glm52/prof/prof_f11b.py:27-46`): unfused = RMSNorm into x2, then the router on the
     raw gate; half-fused = the rstd pass, then the router on the folded gate with the rstd
     epilogue; fused = `fuse_norm=True` (one launch at T <= 4).  The gate is read as [E, H]
-    rows at T <= 16 and as [H, E] above, as in the block.  The roofline counts bytes only
-    (the bf16 MFMA bound of the router's flops is below them at every T)."""
+    rows at T <= 16 and from BOUNDED_ROUTER_MIN_T tokens, as [H, E] in between, as in the
+    block; from BOUNDED_ROUTER_MIN_T tokens every arm also takes the top-8 (`with_topk`),
+    which is what lets the router run its bounded path there.  The roofline counts bytes
+    only (the bf16 MFMA bound of the router's flops is below them at every T)."""
     import torch
 
     from fusion_amd import roofline as RL
+    from fusion_amd.block import BOUNDED_ROUTER_MIN_T
     from fusion_amd.kernels import add_rmsnorm as KN
     from fusion_amd.kernels import lazy_prenorm as KL
 
@@ -417,24 +472,32 @@ def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
     w = (torch.randn(H, device=dev, generator=g) * 0.1 + 1).to(torch.bfloat16)
     gate = (torch.randn(E, H, device=dev, generator=g) * 0.02).to(torch.bfloat16)
     gate_f = KL.fold_weight_nk(gate, w)
-    if T <= 16:
+    # as the block: the gate's rows at decode and from BOUNDED_ROUTER_MIN_T tokens (there
+    # with the top-k, the bounded router's consumer), the [H, E] copy in between
+    topk = T >= BOUNDED_ROUTER_MIN_T
+    if T <= 16 or topk:
         b_raw, b_fold = gate.t(), gate_f.t()
     else:
         b_raw, b_fold = gate.t().contiguous(), gate_f.t().contiguous()
     x2 = torch.empty_like(h1)
     rstd = torch.empty(T, device=dev, dtype=torch.float32)
     lg = torch.empty(T, E, device=dev, dtype=torch.float32)
+    cfg = {}
+    if topk:
+        bias = torch.randn(E, device=dev, generator=g) * 0.01
+        cfg = {"topw": torch.empty(T, 8, device=dev), "correction_bias": bias,
+               "topi": torch.empty(T, 8, dtype=torch.int32, device=dev)}
 
     def unfused():
         KN.norm_only(h1, w, x2, {})
-        KL.launch_router(x2, b_raw, lg, {}, False)
+        KL.launch_router(x2, b_raw, lg, cfg, False)
 
     def half():
         KL.launch_rstd(h1, rstd, {})
-        KL.launch_router(h1, b_fold, lg, {}, False, 1e-5, 0, rstd)
+        KL.launch_router(h1, b_fold, lg, cfg, False, 1e-5, 0, rstd)
 
     def fused():  # one launch at T <= 4 (gate rows); the half-fused pair above that
-        KL.launch_router(h1, b_fold, lg, {}, True)
+        KL.launch_router(h1, b_fold, lg, cfg, True)
 
     u_ms, _ = timed(unfused, steps, warmup)
     h_ms, _ = timed(half, steps, warmup)
@@ -447,7 +510,8 @@ def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
     roof = kc.seconds() * 1e6
     del h1, x2, gate, gate_f, b_raw, b_fold, lg
     return {"unfused_us": round(u_us, 2), "half_fused_us": round(h_us, 2),
-            "fused_us": round(f_us, 2), "gain": round(u_us / min(h_us, f_us), 3),
+            "fused_us": round(f_us, 2), "with_topk": topk,
+            "gain": round(u_us / min(h_us, f_us), 3),
             "roofline_us": round(roof, 2), "roofline_frac": round(roof / min(h_us, f_us), 4),
             "bound": kc.bound()}
 

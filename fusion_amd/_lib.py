@@ -58,6 +58,8 @@ SIGNATURES: dict[str, list] = {
     "glm52_rstd": [_P, _L, _I, _I, _F, _P, _P, _I, _P],
     "glm52_prenorm_router_rows": [_P, _L, _P, _L, _P, _F, _P, _L, _P, _I, _I, _I, _P],
     "glm52_router_logits_rstd": [_P, _L, _P, _L, _L, _I, _P, _P, _L, _P, _L, _I, _I, _I, _P],
+    "glm52_router_rstd": [_P, _L, _P, _L, _L, _I, _P, _P, _L, _P, _L, _P, _P, _L, _P, _L, _I, _I,
+                          _I, _I, _F, _I, _P],
     "glm52_moe_down_merge": [_P, _L, _P, _L, _L, _P, _P, _L, _P, _P, _P, _P, _I, _I, _I, _I, _I,
                              _I, _P],
     "glm52_down_token_major": [_P, _L, _P, _L, _L, _P, _P, _L, _I, _I, _P, _L, _P, _L, _P, _L, _P,

@@ -116,7 +116,7 @@ struct GemmArgs {
   int K;
   int num_valid;
   int group_m;  // tiled mapping: row blocks per swizzle group
-  int stage_k;  // wide mapping: k per LDS stage (64: three-buffer ring, 32: four-buffer ring)
+  int stage_k;  // wide mapping: k per LDS stage (64: a three-buffer ring)
   // stream mapping: an extra expert (the shared one) whose rows are tokens 0 .. x_rows - 1
   // of its own input Ax, with weights Wx ([N, K] like W[e]) and its own output Cx;
   // x_rows = 0: none

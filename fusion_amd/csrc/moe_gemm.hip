@@ -370,12 +370,14 @@ int a_bytes(int num_valid, int a_div, int64_t sa, int k) {
 
 }  // namespace
 
-// variant: 0 = choose (stream when BM == 16; 512-row W tiles when BM is 64 or 128, else the
-// 256-row wide mapping for shapes the 512-row one does not cover; tiled otherwise),
-// 1 = stream, 2 = tiled, 3 = wide with 64-k stages, 4 = wide with 32-k stages, 5 = 512-row
-// W tiles (moe_gemm_wide.hip; block_m in {64, 128}; 256 runs 256 x 256 tiles), 6 =
-// contiguous-run weight stream
-// (moe_gemm_runs.hip; block_m 16).  The default for block_m 16 is 6, else 1.
+// variant: 0 = choose: block_m 16 runs the contiguous-run weight stream (6), and the
+// stream mapping (1) for what it does not cover (k % 512 != 0, output rows not 8-byte
+// aligned); block_m 64, 128 and 256 run the 512-row W tiles (5; 256: 256 x 256 tiles), and
+// at 64 and 128 the 256-row wide mapping (3) for what those do not cover (gated n_out %
+// 256 != 0, plain n_out % 512 != 0, token rows past 2^31 bytes); any other block_m (32)
+// runs the tiled mapping (2).  1 = stream, 2 = tiled, 3 = wide (64-k stages), 5 = 512-row W
+// tiles (moe_gemm_wide.hip), 6 = contiguous-run weight stream (moe_gemm_runs.hip; block_m
+// 16) force one mapping.
 extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, const void* w,
                               int64_t stride_we, int64_t stride_wn, int gate_up_offset,
                               void* c, int64_t stride_cm, const float* topk_weights,
@@ -406,10 +408,11 @@ extern "C" int glm52_moe_gemm(const void* a, int64_t stride_am, int a_row_div, c
                                           : GLM52_EUNSUPPORTED;
     if (rc != GLM52_EUNSUPPORTED || variant == 5) return rc;
   }
-  if (variant == 3 || variant == 4 || auto_wide) {
-    g.stage_k = variant == 4 ? 32 : 64;
+  if (variant == 3 || auto_wide) {
+    g.stage_k = 64;
     return launch_wide(g, capacity, gated != 0, weighted, stream);
   }
+  if (variant == 4 || variant < 0 || variant > 6) return GLM52_EINVAL;
   if (variant == 6 || (variant == 0 && block_m == 16)) {
     // contiguous-run weight stream; shapes it has no instance for fall back to the stream
     // mapping unless it was forced

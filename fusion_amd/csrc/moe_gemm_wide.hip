@@ -279,22 +279,13 @@ int launch_dma(const GemmArgs& a, int capacity, hipStream_t st) {
 
 template <bool GATED, bool WEIGHTED>
 int launch_bm(const GemmArgs& a, int capacity, hipStream_t st) {
-  // stage_k: 64 = three-buffer ring of 64-k stages, 32 = four-buffer ring of 32-k stages
-  if (a.stage_k == 64) {
-    switch (a.BM) {
-      case 64: return launch_dma<64, 64, GATED, WEIGHTED>(a, capacity, st);
-      case 128: return launch_dma<128, 64, GATED, WEIGHTED>(a, capacity, st);
-      default: return GLM52_EUNSUPPORTED;
-    }
+  // a three-buffer ring of 64-k stages
+  if (a.stage_k != 64) return GLM52_EUNSUPPORTED;
+  switch (a.BM) {
+    case 64: return launch_dma<64, 64, GATED, WEIGHTED>(a, capacity, st);
+    case 128: return launch_dma<128, 64, GATED, WEIGHTED>(a, capacity, st);
+    default: return GLM52_EUNSUPPORTED;
   }
-  if (a.stage_k == 32) {
-    switch (a.BM) {
-      case 64: return launch_dma<64, 32, GATED, WEIGHTED>(a, capacity, st);
-      case 128: return launch_dma<128, 32, GATED, WEIGHTED>(a, capacity, st);
-      default: return GLM52_EUNSUPPORTED;
-    }
-  }
-  return GLM52_EUNSUPPORTED;
 }
 
 }  // namespace

@@ -358,7 +358,7 @@ int launch_router_select(const uint16_t* y, int64_t sy, const uint16_t* gate, in
                          float* logits, int64_t sl, void* workspace, int64_t workspace_bytes,
                          const float* bias, float* topw, int64_t stw, int32_t* topi, int64_t sti,
                          int T, int H, int E, int topk, float scale, int norm_prob,
-                         hipStream_t st);
+                         hipStream_t st, const float* rstd = nullptr);
 }  // namespace glm52
 
 // Above this many tokens glm52_router on the gate's rows takes the bounded bf16 path.
@@ -467,27 +467,40 @@ extern "C" int glm52_router_topk(const float* logits, int64_t stride_l, const fl
   GLM52_RETURN_LAUNCH();
 }
 
-// Logits + top-k in two launches (the split-K partials are reduced inside top-k).
-extern "C" int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
-                            int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
-                            void* workspace, int64_t workspace_bytes, const float* bias,
-                            float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i, int T,
-                            int H, int E, int topk, float scale, int norm_prob,
-                            hipStream_t stream) {
+namespace {
+// Logits (times rstd[t] when rstd is given) + top-k.  Gate rows and many tokens: the
+// bounded bf16 logits with the exact rule on each token's candidates (two launches); an
+// operand that path cannot take (misaligned y, a workspace sized for the exact path only)
+// falls through to the exact logits.  Exact path: two launches (the split-K partials are
+// reduced inside top-k), three with rstd (the partials reduced with the epilogue first).
+int router_entry(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                 int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                 void* workspace, int64_t workspace_bytes, const float* bias, float* topw,
+                 int64_t stride_w, int32_t* topi, int64_t stride_i, int T, int H, int E,
+                 int topk, float scale, int norm_prob, const float* rstd, hipStream_t stream) {
   if (topk <= 0 || topk > 8 || topk > E || (E % 4) != 0 || !topw || !topi || stride_w < topk ||
       stride_i < topk)
     return GLM52_EINVAL;
-  if (stride_wk == 1 && !wg_is_f32 && T >= kSelectMinT) {
+  if (T < 0 || H <= 0 || E <= 0 || E > EMAX || !y || !wgt || !logits || stride_l < E)
+    return GLM52_EINVAL;
+  if (stride_wk == 1 && !wg_is_f32 && T >= kSelectMinT && stride_y >= H && (stride_y % 8) == 0 &&
+      (reinterpret_cast<uintptr_t>(y) & 15u) == 0) {
     // gate rows, many tokens: bf16 MFMA logits, the exact rule on each token's candidates
-    if (T < 0 || H <= 0 || E <= 0 || E > EMAX || !y || !wgt || !logits || stride_l < E ||
-        stride_y < H || (stride_y % 8) || (reinterpret_cast<uintptr_t>(y) & 15u))
-      return GLM52_EINVAL;
     const int rc = launch_router_select(static_cast<const uint16_t*>(y), stride_y,
                                         static_cast<const uint16_t*>(wgt), stride_we, logits,
                                         stride_l, workspace, workspace_bytes, bias, topw,
                                         stride_w, topi, stride_i, T, H, E, topk, scale, norm_prob,
-                                        stream);
+                                        stream, rstd);
     if (rc != GLM52_EUNSUPPORTED) return rc;
+  }
+  if (rstd) {
+    const int rc = logits_entry(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits,
+                                stride_l, workspace, workspace_bytes, T, H, E, rstd, stream);
+    if (rc != GLM52_OK || T == 0) return rc;
+    router_topk_kernel<<<(T + 3) / 4, 256, 0, stream>>>(logits, stride_l, nullptr, 1, bias, topw,
+                                                        stride_w, topi, stride_i, T, E, topk,
+                                                        scale, norm_prob);
+    GLM52_RETURN_LAUNCH();
   }
   int ks = 1;
   int rc = launch_logits(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
@@ -497,4 +510,32 @@ extern "C" int glm52_router(const void* y, int64_t stride_y, const void* wgt, in
       logits, stride_l, ks > 1 ? static_cast<const double*>(workspace) : nullptr, ks, bias,
       topw, stride_w, topi, stride_i, T, E, topk, scale, norm_prob);
   GLM52_RETURN_LAUNCH();
+}
+}  // namespace
+
+// Logits + top-k (`norm_router.router_gemm` + `topk_only`).
+extern "C" int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                            int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
+                            void* workspace, int64_t workspace_bytes, const float* bias,
+                            float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i, int T,
+                            int H, int E, int topk, float scale, int norm_prob,
+                            hipStream_t stream) {
+  return router_entry(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                      workspace, workspace_bytes, bias, topw, stride_w, topi, stride_i, T, H, E,
+                      topk, scale, norm_prob, nullptr, stream);
+}
+
+// The same with the half-fused pre-norm epilogue: each logit is its fp32 value times
+// rstd[t] (one fp32 product), and the top-k is taken on those logits.
+extern "C" int glm52_router_rstd(const void* y, int64_t stride_y, const void* wgt,
+                                 int64_t stride_wk, int64_t stride_we, int wg_is_f32,
+                                 const float* rstd, float* logits, int64_t stride_l,
+                                 void* workspace, int64_t workspace_bytes, const float* bias,
+                                 float* topw, int64_t stride_w, int32_t* topi, int64_t stride_i,
+                                 int T, int H, int E, int topk, float scale, int norm_prob,
+                                 hipStream_t stream) {
+  if (T > 0 && !rstd) return GLM52_EINVAL;
+  return router_entry(y, stride_y, wgt, stride_wk, stride_we, wg_is_f32, logits, stride_l,
+                      workspace, workspace_bytes, bias, topw, stride_w, topi, stride_i, T, H, E,
+                      topk, scale, norm_prob, rstd, stream);
 }

@@ -329,13 +329,18 @@ GLM52_DEV void dots_f64(const uint16_t* __restrict__ yrow, const uint16_t* __res
 // One wave per token, four tokens per workgroup; H = NQ * 512.  part: the KS fp32
 // partials, or null when KS == 1 (the logits array then holds L~).  ssy[ks][t] / ssw[ks][e]:
 // the token rows' / gate rows' sums of squares over slice ks (from router_approx_kernel).
+// rstd (optional, the half-fused pre-norm epilogue): every logit is the dot product's fp32
+// value times rstd[t] (one fp32 product) -- the exact rule's logit fl(fl(dot) * r) for the
+// candidates, fl(L~ * r) elsewhere.  With |L~ - dot| <= B, |fl(L~ r) - fl(fl(dot) r)| <=
+// r B (1 + 2^-23) + 3 * 2^-24 |L~ r|, which B' = r B (1 + 2^-20) + 2^-21 |fl(L~ r)| covers;
+// the candidates are then chosen from B' exactly as from B.
 template <int NQ>
 __global__ __launch_bounds__(256) void router_select_kernel(
     const uint16_t* __restrict__ y, int64_t sy, const uint16_t* __restrict__ gate, int64_t sg,
     const float* __restrict__ part, int KS, const float* __restrict__ ssw,
     const float* __restrict__ ssy, const float* __restrict__ bias, float* __restrict__ logits,
     int64_t sl, float* __restrict__ topw, int64_t stw, int32_t* __restrict__ topi, int64_t sti,
-    int T, int E, int topk, float scale, int norm_prob) {
+    int T, int E, int topk, float scale, int norm_prob, const float* __restrict__ rstd) {
   __shared__ float sel_s[4][8];
   __shared__ int sel_i[4][8];
   __shared__ int cand[4][kMaxE];
@@ -348,6 +353,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(
 
   float bv[4];
   load_bias(bias, E, bv);
+  const float rs = rstd && t_ok ? rstd[t] : 1.0f;
 
   // L~, the gate rows' sums of squares of the lane's experts and the token row's sum of
   // squares: the K slices' values loaded eight at a time (all in flight), summed in order
@@ -386,11 +392,13 @@ __global__ __launch_bounds__(256) void router_select_kernel(
     ol[j] = 0u;
     oh[j] = 0u;
     if (t_ok && e < E) {
-      const float l = (float)la[j];
-      if (part) logits[t * sl + e] = l;
+      const float l0 = (float)la[j];
+      const float l = rstd ? l0 * rs : l0;
+      if (part || rstd) logits[t * sl + e] = l;
       const float sw2 = sw[j] * (1.0f + 0x1p-10f);
-      const float bnd = 2.5f * 0x1p-16f * __fsqrt_rn(sy2 * sw2) * (1.0f + 0x1p-20f) +
-                        0x1p-21f * fabsf(l) + 1e-30f;
+      float bnd = 2.5f * 0x1p-16f * __fsqrt_rn(sy2 * sw2) * (1.0f + 0x1p-20f) +
+                  0x1p-21f * fabsf(l0) + 1e-30f;
+      if (rstd) bnd = bnd * rs * (1.0f + 0x1p-20f) + 0x1p-21f * fabsf(l) + 1e-30f;
       const float b = bv[j];
       const float d = 0x1p-17f + fabsf(b) * 0x1p-22f;
       float lo = -INFINITY, hi = INFINITY;
@@ -450,7 +458,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(
       double v = d[0];
 #pragma unroll
       for (int c = 1; c < 8; ++c) v = lane == c ? d[c] : v;
-      clg[wv][i + lane] = (float)v;
+      clg[wv][i + lane] = rstd ? (float)v * rs : (float)v;
     }
   }
   for (; i < nc; i += 4) {
@@ -462,7 +470,7 @@ __global__ __launch_bounds__(256) void router_select_kernel(
       double v = d[0];
 #pragma unroll
       for (int c = 1; c < 4; ++c) v = lane == c ? d[c] : v;
-      clg[wv][i + lane] = (float)v;
+      clg[wv][i + lane] = rstd ? (float)v * rs : (float)v;
     }
   }
   __builtin_amdgcn_s_waitcnt(0xc07f);
@@ -528,15 +536,16 @@ int launch_router_select(const uint16_t* y, int64_t sy, const uint16_t* gate, in
                          float* logits, int64_t sl, void* workspace, int64_t workspace_bytes,
                          const float* bias, float* topw, int64_t stw, int32_t* topi, int64_t sti,
                          int T, int H, int E, int topk, float scale, int norm_prob,
-                         hipStream_t st) {
+                         hipStream_t st, const float* rstd) {
   if ((H != 4096 && H != 6144 && H != 8192) || E > kMaxE || E < topk || (E % 4) ||
       (sg % 8) || sg < H || (reinterpret_cast<uintptr_t>(gate) & 15u))
     return GLM52_EUNSUPPORTED;
   if (T == 0) return GLM52_OK;
   const int ks = select_ks(T, H);
+  // a workspace sized for the exact path only: the caller falls back to it
   if (!workspace || workspace_bytes < router_select_workspace_bytes(T, H, E) ||
       (reinterpret_cast<uintptr_t>(workspace) & 15u))
-    return GLM52_EINVAL;
+    return GLM52_EUNSUPPORTED;
   float* ssw = static_cast<float*>(workspace);
   float* ssy = ssw + (int64_t)ks * E;
   float* part = ks > 1 ? reinterpret_cast<float*>(
@@ -556,15 +565,15 @@ int launch_router_select(const uint16_t* y, int64_t sy, const uint16_t* gate, in
   switch (H / 512) {
     case 8:
       router_select_kernel<8><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
-                                                  sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
+                                                  sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob, rstd);
       break;
     case 12:
       router_select_kernel<12><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
-                                                   sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
+                                                   sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob, rstd);
       break;
     default:
       router_select_kernel<16><<<nb, 256, 0, st>>>(y, sy, gate, sg, part, ks, ssw, ssy, bias, logits,
-                                                   sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob);
+                                                   sl, topw, stw, topi, sti, T, E, topk, scale, norm_prob, rstd);
       break;
   }
   GLM52_RETURN_LAUNCH();

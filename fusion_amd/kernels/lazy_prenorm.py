@@ -12,7 +12,9 @@ Launchers, with the reference's names and arguments:
     launch_rstd(x, rstd, cfg, eps)                         (`lazy_prenorm.py:371-390`)
     launch_router(a, b, c, cfg, fuse_norm, eps, sq_mode, rstd)        (`:457-489`)
         c [M, N] fp32 = (a @ b) * rstd   (rstd given, or computed here when fuse_norm);
-        the logits rounded to fp32 under the router's exact rule, then one fp32 product
+        the logits rounded to fp32 under the router's exact rule, then one fp32 product;
+        with cfg["topw"] / cfg["topi"] also their top-k (the bounded router on gate rows
+        from 17 tokens: `glm52_router_rstd`)
     launch_moe_gateup(a, b, c, sorted_token_ids, expert_ids, num_tokens_post_padded,
                       num_valid_tokens, top_k, cfg, fuse_norm, eps, sq_mode, rstd)
         c [T * top_k, N] bf16 = bf16((a[f / top_k] @ b[e]^T) * rstd[f / top_k])
@@ -66,10 +68,20 @@ def launch_rstd(x, rstd, cfg, eps: float = 1e-5, rstd_flat=None, repeat: int = 1
 
 def launch_router(a, b, c, cfg, fuse_norm: bool, eps: float = 1e-5, sq_mode: int = 0,
                   rstd=None):
-    """`a`: [M,K] bf16.  `b`: [K,N] bf16.  `c`: [M,N] fp32."""
+    """`a`: [M,K] bf16.  `b`: [K,N] bf16.  `c`: [M,N] fp32.
+
+    With `cfg["topw"]` and `cfg["topi"]` ([M, k] fp32 / int32 outputs) the launch also takes
+    the router's top-k of these logits (`topk_only`, with cfg's `correction_bias`, `scale`
+    and `NORM_PROB`).  On a gate read as rows (`b` the transposed view of [N, K]) from 17
+    tokens that runs the bounded router: ids and weights are the exact rule's bit for bit,
+    and `c` is exact for each token's candidate experts (every selected one among them) and
+    within the proven bound, times rstd, elsewhere."""
     M = a.shape[0]
     if M == 0:
         return  # an empty batch: nothing to launch
+    if cfg.get("topw") is not None or cfg.get("topi") is not None:
+        _router_topk(a, b, c, cfg, fuse_norm, eps, rstd)
+        return
     if (fuse_norm or rstd is not None) and M <= 4 and b.stride(0) == 1:
         _rows_router(a, b, c, rstd, eps)
         return
@@ -88,6 +100,36 @@ def launch_router(a, b, c, cfg, fuse_norm: bool, eps: float = 1e-5, sq_mode: int
     _lib.call("glm52_router_logits_rstd", _lib.ptr(a), a.stride(0), _lib.ptr(b), b.stride(0),
               b.stride(1), int(b.dtype == torch.float32), _lib.ptr(rstd), _lib.ptr(c),
               c.stride(0), _lib.ptr(ws), need, M, K, N, _lib.stream())
+
+
+def _router_topk(a, b, c, cfg, fuse_norm, eps, rstd):
+    """Logits (times rstd when given or when `fuse_norm` asks for the statistic) and their
+    top-k: `glm52_router_rstd`, or the block's router when there is no epilogue."""
+    topw, topi = cfg.get("topw"), cfg.get("topi")
+    if topw is None or topi is None:
+        raise ValueError("cfg needs both topw and topi for the router's top-k")
+    if rstd is None and not fuse_norm:
+        _nr.router(a, b, c, topw, topi, cfg)
+        return
+    M, K = a.shape
+    if rstd is None:
+        rstd = torch.empty(M, dtype=torch.float32, device=a.device)
+        launch_rstd(a, rstd, cfg, eps)
+    _nr._check_router_operands(a, b, c)
+    _lib.require_gpu(rstd, topw, topi)
+    if rstd.dtype != torch.float32 or not rstd.is_contiguous() or rstd.numel() < M:
+        raise ValueError("rstd must be a contiguous fp32 tensor of M values")
+    bias = cfg.get("correction_bias")
+    if bias is not None and (bias.dtype != torch.float32 or not bias.is_contiguous()):
+        raise ValueError("correction_bias must be a contiguous fp32 tensor")
+    N = b.shape[1]
+    ws, need = _nr._workspace(M, K, N, a.device, cfg, b, select=True)
+    _lib.call("glm52_router_rstd", _lib.ptr(a), a.stride(0), _lib.ptr(b), b.stride(0),
+              b.stride(1), int(b.dtype == torch.float32), _lib.ptr(rstd), _lib.ptr(c),
+              c.stride(0), _lib.ptr(ws), need, _lib.ptr(bias), _lib.ptr(topw), topw.stride(0),
+              _lib.ptr(topi), topi.stride(0), M, K, N, topi.shape[1],
+              float(cfg.get("scale", 2.5)), int(bool(cfg.get("NORM_PROB", True))),
+              _lib.stream())
 
 
 def _rows_router(a, b, c, rstd, eps):

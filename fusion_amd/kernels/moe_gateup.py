@@ -12,11 +12,13 @@ conventions (`glm52/kernels/REFERENCES.md:41-51`): A rows are gathered with
 
 `cfg["BLOCK_M"]` must equal the layout's block size (checked).  `cfg["variant"]` may
 force "stream" (weight-streaming decode mapping), "tiled" (register-staged LDS tiles),
-"wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages), "wide32"
-(the same with 32-k stages), "w512" (512-row W tiles on the 32x32x16 MFMA, 32-k stages) or
-"runs" (the decode weight stream read as contiguous 1 KB row runs through LDS); by default
-BM = 16 runs "runs" (falling back to "stream" for shapes it does not cover), BM in
-{64, 128} runs "w512" (falling back to "wide") and BM = 32 "tiled".
+"wide" (256-row W tiles fed by direct global -> LDS loads through 64-k stages), "w512"
+(512-row W tiles on the 32x32x16 MFMA, 32-k stages; 256 x 256 tiles at BM = 256) or
+"runs" (the decode weight stream read as contiguous 1 KB row runs through LDS).  By
+default BM = 16 runs "runs", and "stream" for the shapes it does not cover (K % 512 != 0,
+output rows not 8-byte aligned); BM in {64, 128, 256} runs "w512", and at 64 and 128
+"wide" for the shapes it does not cover (gated N % 256 != 0, plain N % 512 != 0); any
+other BM (32) runs "tiled".
 """
 
 from __future__ import annotations
@@ -25,8 +27,7 @@ import torch
 
 from .. import _lib
 
-VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "wide32": 4, "w512": 5,
-            "runs": 6}
+VARIANTS = {None: 0, "auto": 0, "stream": 1, "tiled": 2, "wide": 3, "w512": 5, "runs": 6}
 
 
 def check_layout(sorted_token_ids, expert_ids, num_tokens_post_padded, block_m: int) -> int:
@@ -210,9 +211,8 @@ def smem_bytes(cfg: dict, fused: bool) -> int:
         return 8192
     if variant == "w512" or (variant is None and bm in (64, 128, 256)):
         return 5 * (256 + bm) * 32 * 2 if bm == 256 else 4 * (512 + bm) * 32 * 2
-    if variant in ("wide", "wide32"):
-        stages, bk = (4, 32) if variant == "wide32" else (3, 64)
-        return stages * (256 + bm) * bk * 2 + 4 * bm
+    if variant == "wide":
+        return 3 * (256 + bm) * 64 * 2 + 4 * bm
     nb = 128
     return 2 * (bm + nb) * (64 + 8) * 2 + 4 * bm
 

@@ -69,16 +69,17 @@ def packed_weight(b: torch.Tensor, splits: int = 1) -> torch.Tensor:
     """The packed copy of B ([K, N] bf16, cut into `splits` K slices) the prefill mapping
     reads, cached.
 
-    A hit needs the tensor that was packed to be alive (and to share B's storage): while
-    it lives its memory cannot be handed to another tensor, so an equal address, shape,
-    strides and version counter mean equal contents.  Once it is freed the entry is dead,
-    even if a new weight later lands at the same address with the same version."""
+    A hit needs the tensor that owns B's storage (B itself, or the tensor B is a view of)
+    to be alive: while it lives its memory cannot be handed to another tensor, so an equal
+    address, shape, strides and version counter mean equal contents.  A caller that passes
+    a fresh view of the same weight every call (`w.t()`) keeps hitting, since the owner
+    stays alive.  Once the owner is freed the entry is dead, even if a new weight later
+    lands at the same address with the same version."""
     key = (b.device.index, b.data_ptr(), tuple(b.shape), tuple(b.stride()), b._version, splits)
     hit = _PACKED.get(key)
     if hit is not None:
         src = hit[0]()
-        if src is not None and (src is b or src.untyped_storage().data_ptr()
-                                == b.untyped_storage().data_ptr()):
+        if src is not None and src.untyped_storage().data_ptr() == b.untyped_storage().data_ptr():
             _PACKED.move_to_end(key)
             return hit[1]
         del _PACKED[key]
@@ -89,7 +90,8 @@ def packed_weight(b: torch.Tensor, splits: int = 1) -> torch.Tensor:
     out = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=b.device)
     _lib.call("glm52_oproj_pack", _lib.ptr(b), b.stride(0), b.stride(1), K, N, int(splits),
               _lib.ptr(out), _lib.stream())
-    _PACKED[key] = (weakref.ref(b), out)
+    owner = b._base if b._base is not None else b
+    _PACKED[key] = (weakref.ref(owner), out)
     while len(_PACKED) > _PACK_CACHE_SIZE:
         _PACKED.popitem(last=False)
     return out

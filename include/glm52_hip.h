@@ -57,7 +57,9 @@ int64_t glm52_router_workspace_bytes(int T, int H, int E);
  * exclude from the top k -- get the exact logit: ids and weights equal the exact rule's
  * bit for bit; logits are exact for the candidates and within the bound elsewhere.  That
  * path needs glm52_router_select_workspace_bytes(T, H, E) bytes of workspace (16-byte
- * aligned), H of 4096, 6144 or 8192 (else the exact mappings run), E % 4 == 0. */
+ * aligned), H of 4096, 6144 or 8192 and E % 4 == 0; with a smaller workspace (the size
+ * glm52_router_workspace_bytes gives) or a y that is not 16-byte aligned the exact
+ * mappings run instead, with every logit exact. */
 int64_t glm52_router_select_workspace_bytes(int T, int H, int E);
 int glm52_router(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
                  int64_t stride_we, int wg_is_f32, float* logits, int64_t stride_l,
@@ -301,6 +303,19 @@ int glm52_router_logits_rstd(const void* y, int64_t stride_y, const void* wgt, i
                              int64_t stride_we, int wg_is_f32, const float* rstd, float* logits,
                              int64_t stride_l, void* workspace, int64_t workspace_bytes, int T,
                              int H, int E, hipStream_t stream);
+/* glm52_router_rstd: glm52_router with the same epilogue -- the router GEMM with USE_RSTD
+ *     (glm52/kernels/lazy_prenorm.py:229-330, launch_router :457-489) followed by the
+ *     top-k the block's router takes on its logits (topk_only, glm52/kernels/
+ *     norm_router.py:352-354): each logit is its fp32 value times rstd[t], and ids and
+ *     weights are the exact rule's on those logits.  On the gate's rows from 17 tokens the
+ *     bounded path of glm52_router runs (its workspace query, its logits semantics: exact
+ *     times rstd for the candidates, within the bound times rstd elsewhere). */
+int glm52_router_rstd(const void* y, int64_t stride_y, const void* wgt, int64_t stride_wk,
+                      int64_t stride_we, int wg_is_f32, const float* rstd, float* logits,
+                      int64_t stride_l, void* workspace, int64_t workspace_bytes,
+                      const float* bias, float* topw, int64_t stride_w, int32_t* topi,
+                      int64_t stride_i, int T, int H, int E, int topk, float scale,
+                      int norm_prob, hipStream_t stream);
 
 /* The down GEMM with the atomic expert merge: fusion #8(a) / #9(a), replaces
  * moe_down_merge.launch_down(fuse_merge=True) (glm52/kernels/moe_down_merge.py:427-476,

@@ -447,7 +447,7 @@ def _close(got: torch.Tensor, ref: torch.Tensor, what: str):
 
 @pytest.mark.parametrize("bm,variant", [(16, "stream"), (32, "tiled"), (64, "tiled"),
                                         (128, "tiled"), (64, "stream"), (64, "wide"),
-                                        (128, "wide"), (64, "wide32"), (128, "wide32"),
+                                        (128, "wide"),
                                         (64, "w512"), (128, "w512"), (128, None)])
 def test_grouped_gemms_small(gpu, bm, variant):
     say(f"grouped gemm small bm={bm} {variant}")
@@ -482,7 +482,7 @@ def test_grouped_gemm_full_width(gpu):
     ag, w13g, w2g = a.to(gpu), w13.to(gpu), w2.to(gpu)
     act_ref = _gateup_ref(a, w13, ids, k, I, True)
     for bm, variant in ((16, "stream"), (16, "runs"), (32, "tiled"), (64, "wide"), (128, "wide"),
-                        (64, "wide32"), (64, "w512"), (128, "w512")):
+                        (64, "w512"), (128, "w512")):
         say(f"grouped gemm full width bm={bm} {variant}")
         sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
         cfg = {"BLOCK_M": bm, "variant": variant}
@@ -495,11 +495,13 @@ def test_grouped_gemm_full_width(gpu):
         _close(y, _down_ref(act, w2, ids, tw), f"w2 {variant}")
 
 
-@pytest.mark.parametrize("bm", [64, 128])
+@pytest.mark.parametrize("bm", [64, 128, 256])
 @pytest.mark.parametrize("T,E,H,I", [(300, 8, 512, 256), (200, 8, 6144, 2048)])
 def test_packed_w512_matches_unpacked(gpu, bm, T, E, H, I):
     """The prefill GEMM on packed weights: the same bits as on the weights in place, for the
-    gated w13 + SwiGLU, the weighted w2 and the plain (shared-expert) w2."""
+    gated w13 + SwiGLU, the weighted w2 and the plain (shared-expert) w2.  At block size 256
+    (the 256 x 256 tiles) T = 300 gives each expert a second block of 44 real rows, so the
+    waves whose 128 token rows are all padding take the path that only stages loads."""
     say(f"packed w512 bm={bm} T={T} E={E} H={H} I={I}")
     k = 8  # every slot of the layout is routed (E >= k distinct ids per token)
     a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 60 + bm, gpu)
@@ -528,6 +530,49 @@ def test_packed_w512_matches_unpacked(gpu, bm, T, E, H, I):
     assert torch.equal(y_p, y)
     assert torch.equal(y0_p, y0)
     _close(act, _gateup_ref(a, w13, ids, k, I, True), "w13 (packed path reference)")
+    _close(y, _down_ref(act, w2, ids, tw), "w2 weighted (packed path reference)")
+
+
+@pytest.mark.parametrize("bm", [64, 128, 256])
+@pytest.mark.parametrize("T", [77, 300])
+def test_moe_gemm_packed_shared_matches_separate_launches(gpu, bm, T):
+    """Routed + shared expert in one prefill launch (`moe_gemm_packed_shared`, the shared
+    expert's row blocks after each XCD's routed items): the same bits as the routed launch
+    and a separate launch over the shared expert's one-expert layout, with T rows not a
+    multiple of the block size (the last shared block partly padding)."""
+    from fusion_amd.block import shared_layout
+
+    say(f"moe_gemm_packed_shared bm={bm} T={T}")
+    E, H, I, k = 8, 512, 256, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 500 + T + bm, gpu)
+    g = torch.Generator().manual_seed(900 + T)
+    w13s = (torch.randn(1, 2 * I, H, generator=g) * 0.05).to(BF16).to(gpu)
+    w2s = (torch.randn(1, H, I, generator=g) * 0.05).to(BF16).to(gpu)
+    ag = a.to(gpu)
+    w13p, w2p = KG.pack_w512(w13.to(gpu), I, I, True), KG.pack_w512(w2.to(gpu), H, 0, False)
+    w13sp, w2sp = KG.pack_w512(w13s, I, I, True), KG.pack_w512(w2s, H, 0, False)
+    twf = tw.reshape(-1).contiguous().to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
+    ssti, seids, sntp = shared_layout(T, bm, gpu)
+    cfg = {"BLOCK_M": bm}
+    R = T * k
+    act, act_s = torch.empty(R, I, dtype=BF16, device=gpu), torch.empty(T, I, dtype=BF16, device=gpu)
+    KG.moe_gemm_packed(ag, k, w13p, act, None, sti, eids, ntp, R, I, True, cfg)
+    KG.moe_gemm_packed(ag, 1, w13sp, act_s, None, ssti, seids, sntp, T, I, True, cfg)
+    y, s_out = torch.empty(R, H, dtype=BF16, device=gpu), torch.empty(T, H, dtype=BF16, device=gpu)
+    KG.moe_gemm_packed(act, 1, w2p, y, twf, sti, eids, ntp, R, H, False, cfg)
+    KG.moe_gemm_packed(act_s, 1, w2sp, s_out, None, ssti, seids, sntp, T, H, False, cfg)
+    act2, act_s2 = torch.full_like(act, float("nan")), torch.full_like(act_s, float("nan"))
+    KG.moe_gemm_packed_shared(ag, k, w13p, act2, None, sti, eids, ntp, R, I, True, cfg, ag, w13sp,
+                              act_s2)
+    y2, s_out2 = torch.full_like(y, float("nan")), torch.full_like(s_out, float("nan"))
+    KG.moe_gemm_packed_shared(act2, 1, w2p, y2, twf, sti, eids, ntp, R, H, False, cfg, act_s2,
+                              w2sp, s_out2)
+    torch.cuda.synchronize()
+    assert torch.equal(act2, act) and torch.equal(act_s2, act_s)
+    assert torch.equal(y2, y) and torch.equal(s_out2, s_out)
+    _close(act_s, _gateup_ref(a, w13s.cpu(), torch.zeros(T, 1, dtype=torch.int32), 1, I, True),
+           "shared w13 (fp32 reference)")
 
 
 @pytest.mark.parametrize("T", [1, 3, 16, 40])

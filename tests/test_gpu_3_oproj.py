@@ -133,3 +133,15 @@ def test_oproj_pack_cache_misses_a_new_weight_at_a_freed_address(gpu):
     torch.cuda.synchronize()
     assert not torch.equal(out, first)
     torch.testing.assert_close(out.float(), a.float() @ b2.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_oproj_pack_cache_hits_fresh_views(gpu):
+    """A caller passing a fresh view of one weight each call (`w.t()`) reuses the packed
+    copy: the cache keeps the view's base alive-checked, not the short-lived view."""
+    K, N = 2048, N_OUT
+    bt = (torch.randn(N, K, device=gpu) * 0.02).to(BF16)
+    p1 = KO.packed_weight(bt.t())
+    p2 = KO.packed_weight(bt.t())
+    assert p1 is p2
+    bt.mul_(2.0)  # an in-place update bumps the shared version counter: repacked
+    assert KO.packed_weight(bt.t()) is not p1

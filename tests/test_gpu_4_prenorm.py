@@ -156,3 +156,45 @@ def test_norm_router_no_x2_leaves_x2(gpu):
     torch.cuda.synchronize()
     assert torch.equal(lg2, lg)
     assert bool((sentinel == 3.0).all())
+
+
+@pytest.mark.parametrize("T", [5, 17, 1000, 2048, 4100])
+def test_prenorm_router_topk(gpu, T):
+    """The router with the rstd epilogue and its top-k (`glm52_router_rstd`) on a gate read
+    as rows: from 17 tokens the bounded router, below it the exact logits (T = 5).  Ids and weights bit for bit against the
+    exact rule on the oracle's pre-norm logits (exact logit, one fp32 multiply by rstd);
+    the selected logits exact; every other logit within rstd times the bounded router's
+    bound.  fuse_norm (the statistic computed here) gives the same bits as rstd given."""
+    say(f"prenorm router + top-k T={T}")
+    h, w, g = _h(T, gpu, 300 + T)
+    gate = (torch.randn(ER, H, device=gpu, generator=g) * 0.02).to(BF16)
+    gate_f = KL.fold_weight_nk(gate, w)
+    bias = torch.randn(ER, device=gpu, generator=g) * 0.01
+    rstd = torch.empty(T, device=gpu)
+    KL.launch_rstd(h, rstd, {}, EPS)
+    out = {}
+    for name, fuse in (("half", False), ("fused", True)):
+        lg = torch.full((T, ER), float("nan"), device=gpu)
+        tw = torch.empty(T, 8, device=gpu)
+        ti = torch.empty(T, 8, dtype=torch.int32, device=gpu)
+        cfg = {"topw": tw, "topi": ti, "correction_bias": bias}
+        KL.launch_router(h, gate_f.t(), lg, cfg, fuse, EPS, 0, None if fuse else rstd)
+        out[name] = (lg, tw, ti)
+    torch.cuda.synchronize()
+    for a, b in zip(out["half"], out["fused"]):
+        assert torch.equal(a, b)
+    lg, tw, ti = (t.cpu().numpy() for t in out["half"])
+    r_o = O.rstd_exact(h.cpu(), EPS)
+    want = O.prenorm_router(h.cpu(), gate_f.t().contiguous().cpu(), r_o)
+    w_o, ids_o, _ = O.router_select(want, bias.cpu().numpy())
+    assert np.array_equal(ti, ids_o)
+    assert np.array_equal(tw, w_o)
+    sel = np.take_along_axis(lg, ids_o.astype(np.int64), 1)
+    assert np.array_equal(sel, np.take_along_axis(want, ids_o.astype(np.int64), 1))
+    hn = np.sqrt((h.cpu().double().numpy() ** 2).sum(1))[:, None]
+    gn = np.sqrt((gate_f.cpu().double().numpy() ** 2).sum(1))[None, :]
+    bound = (r_o.astype(np.float64)[:, None] * 1.375 * 2.0 ** -16 * hn * gn
+             + 2.0 ** -19 * np.abs(want) + 1e-30)
+    ratio = np.abs(lg.astype(np.float64) - want) / bound
+    say(f"  max |error| / bound = {ratio.max():.3e}, exact fraction {(lg == want).mean():.3f}")
+    assert ratio.max() <= 1.0
