@@ -10,13 +10,18 @@ and 8192 (configurations 2-4, the last with the skewed router bias, whose expert
 are reported with it) are under `per_T`.  Timing follows the reference's `bench_chain`
 (`glm52/common.py:73-122`): one cache flush (1 GiB, larger than the 256 MB Infinity
 Cache) before every step, never inside it, HIP events around the step, eager launches;
+each size first runs untimed blocks for 50 ms (the GPU's clocks settle over ~30 ms of load
+after an idle gap) and then the W warm-up steps before its K timed steps;
 decode sizes also report the replay of a captured HIP graph (`graph_us`).  Each size
 reports the reference's timing record: median, p10, p90, mean and min over the timed
 steps and the median of the same steps without the flush; the headline size also lists
 every step.  The dominant kernel -- the block's w13 + SwiGLU launch, which at T <= 4 also
 derives the routing and runs the shared expert -- is timed with events on its stream
 around it inside whole blocks (after the flush and the front end, before the tail): that
-mean is the `roofline` object's `avg_us`; the same launch timed alone is `solo_us`.  Its
+mean is the `roofline` object's `avg_us`; the same launch timed alone is `solo_us`.  HIP
+events around one launch read 4-6 us more than a kernel trace's begin-to-end of the same
+dispatch (their marker packets and the dispatch's own set-up and completion), so `avg_us`
+is the conservative figure.  Its
 HBM traffic comes
 from two `rocprofv3 --pmc` runs of a child process (`--pmc-child`), scaled by a plain
 copy of known size.  The CPU baseline is the oracle's restatement of
@@ -45,8 +50,7 @@ def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    # 25 untimed steps, as the reference's bench_chain: the first ~25 blocks of a fresh
-    # process run slower (measured at T = 1: 128-130 us, then 121-122 us)
+    # 25 untimed steps, as the reference's bench_chain (after the 50 ms clock settle)
     ap.add_argument("--warmup", type=int, default=25)
     ap.add_argument("--tokens", default="1,256,2048,8192",
                     help="token counts; the first is the headline (configuration 1 is T=1)")
@@ -128,6 +132,21 @@ def main() -> int:
     def flush():
         flush_buf.zero_()
 
+    def settle(fn, ms=SETTLE_MS):
+        """Untimed steps (each after the flush) until `ms` of them have run: after an idle
+        gap the GPU's clocks take ~30 ms of load to settle (the T = 1 w13 launch runs 78 us
+        after 76 ms idle, 70-72 us 30 ms later), which W steps of decode alone do not
+        cover."""
+        t_end = time.perf_counter() + ms * 1e-3
+        n = 0
+        while time.perf_counter() < t_end or n == 0:
+            for _ in range(8):
+                flush()
+                fn()
+            torch.cuda.synchronize()
+            n += 8
+        return n
+
     def timed(fn, steps, warmup, do_flush=True):
         for _ in range(warmup):
             flush()
@@ -183,6 +202,7 @@ def main() -> int:
         # the headline times eager launches, as the reference's bench_chain does; decode
         # sizes also time a captured HIP graph of the same chain (reported, not headline:
         # on this ROCm its replay adds launch gaps between the nodes)
+        n_settle = settle(lambda: blk(x, r))
         ms, wall = timed(lambda: blk(x, r), args.steps, args.warmup)
         # the reference's no-flush median (`glm52/common.py:95-110`), same steps
         nf_ms, _ = timed(lambda: blk(x, r), args.steps, 2, do_flush=False)
@@ -202,6 +222,7 @@ def main() -> int:
         med_us = st["p50_us"]
         rec = {
             "us_per_block": med_us,
+            "settle_steps": n_settle,
             "p10_us": st["p10_us"],
             "p90_us": st["p90_us"],
             "us_mean": st["mean_us"],
@@ -290,6 +311,8 @@ def step_stats(ms: list) -> dict:
             "mean_us": round(statistics.fmean(ts) * 1e3, 2), "min_us": round(ts[0] * 1e3, 2)}
 
 
+# untimed blocks before each size's W warm-up steps, in ms of wall time (clock settle)
+SETTLE_MS = 50.0
 PMC_LAUNCHES = 3
 COPY_KIB = 262144  # the child's plain copies: 256 MiB read and 256 MiB written each
 

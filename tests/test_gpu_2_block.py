@@ -130,11 +130,19 @@ def assert_block_close(out, exact, faithful, y3=None, s=None):
       framework path, for the whole batch and for every token row.
     """
     o, x = out.float(), exact.float()
-    bound = 2e-2 + 2e-2 * x.abs()
+    strict = 2e-2 + 2e-2 * x.abs()
+    bound = strict
     if y3 is not None:
         bound = bound + half_ulp_bf16(y3).sum(1)
     if s is not None:
         bound = bound + half_ulp_bf16(s)
+    # the elements past the strict north-star bound, for the device output and for the
+    # framework path (the reference's chain restated on the CPU): every device one must lie
+    # within the widening, which the assertion below checks on all elements
+    n_dev = int(((o - x).abs() > strict).sum())
+    n_fw = int(((faithful.float() - x).abs() > strict).sum())
+    say(f"  past the strict rtol/atol 2e-2 bound: device {n_dev}, framework path {n_fw} "
+        f"of {o.numel()} elements")
     excess = (o - x).abs() - bound
     worst = int(excess.argmax())
     assert float(excess.max()) <= 0, (
@@ -145,6 +153,7 @@ def assert_block_close(out, exact, faithful, y3=None, s=None):
     f = faithful.float()
     row_err = (o - f).abs().amax(1) / f.abs().amax(1)
     assert float(row_err.max()) <= 2e-2
+    return n_dev, n_fw
 
 
 def i32_sha(a) -> str:
@@ -215,10 +224,10 @@ def test_block_parity(gpu, weights, packed, T, bias):
     assert torch.equal(out2, out)
 
 
-@pytest.mark.parametrize("T", [1, 256, 2048])
+@pytest.mark.parametrize("T", [1, 256, 2048, 8192])
 def test_block_graph_replay(gpu, packed, T):
     say(f"graph replay T={T}")
-    fe = front_end(T)
+    fe = front_end(T, bias="zipf" if T == 8192 else "normal")
     x, r = fe.x.to(gpu), fe.r.to(gpu)
     blk = MoEBlock(T, fe.w_norm.to(gpu), fe.wgt.to(gpu), fe.bias.to(gpu), packed)
     eager = blk(x, r).clone()
