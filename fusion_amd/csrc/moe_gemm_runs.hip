@@ -197,9 +197,12 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // take runs of C consecutive items, so the outputs that share a 128-byte line --
   // consecutive items of a layout block -- are written through one L2 instead of several.
   // C = 32 (all of an XCD's share of the round) for the gated launches and 4 (one line of
-  // 64 outputs) for the plain ones: measured at T = 256, w13 2235 -> 2080 us and the
-  // block 3614 -> 3406 us.  The last, partial round keeps the issue order.
-  constexpr int C = GATED ? 32 : 4;
+  // 64 outputs) for the plain ones on weights in place: measured at T = 256, w13 2235 ->
+  // 2080 us and the block 3614 -> 3406 us.  The plain launch on packed weights keeps the
+  // issue order (C = 1: consecutive items on consecutive XCDs), each item one packed slot:
+  // at T = 256 its w2 launch runs 1349 us against 1402 (C = 4), 1417 (C = 2) and 1407 us
+  // (C = 8), interleaved in one process.  The last, partial round keeps the issue order.
+  constexpr int C = GATED ? 32 : (PACKED ? 1 : 4);
   auto place = [&](int it) {
     if (ROUTE) return it;
     const int G = (int)gridDim.x;
