@@ -158,6 +158,9 @@ struct GemmArgs {
   // with packed bf16 atomics into row f / merge_topk of C (non-gated only; the 512-row
   // tile and contiguous-run mappings); 0: the result is stored into row f
   int merge_topk;
+  // 512-row tile mapping: the set of per-XCD item counters this launch deals its items
+  // from (set by the launcher)
+  int deal_set;
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

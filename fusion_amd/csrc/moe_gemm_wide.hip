@@ -29,6 +29,7 @@
 // once and served to the others from the XCD's L2.
 #include "moe_gemm.h"
 
+#include <atomic>
 #include <type_traits>
 
 using namespace glm52;
@@ -347,6 +348,23 @@ GLM52_DEV int w512_chunk(int l) { return (l & 3) ^ (((l >> 2) >> 2) & 3); }
 // tile heights read one packed copy.  A stage is 32 KB, so five fit in LDS: four in flight
 // while one is multiplied.  A tile of 256 tokens covers most experts' rows at prefill
 // sizes in one item, so most W tiles are streamed by one workgroup only.
+//
+// Dealing.  Each XCD owns a contiguous share of the items (its routed items, then its
+// share of the extra expert's), so the W tiles and token rows its workgroups share stay in
+// its L2.  A workgroup (XCD blockIdx.x % 8) takes its first item by its index and each
+// next one from its XCD's counter, fetched while the current item runs; once its XCD's
+// items are all taken it takes those of the next XCDs.  The items differ in cost (L2
+// hits, non-temporal tiles, real rows), so a fixed round-robin deal left the workgroups of
+// one XCD finishing hundreds of microseconds apart.  Every item writes its own outputs:
+// the results do not depend on which workgroup runs it.  The counters of one launch are a
+// set of kDealSets; the launcher gives consecutive launches consecutive sets, and the
+// last workgroup out clears its set, so launches that overlap on one GPU use different
+// sets unless kDealSets launches apart (a captured graph keeps the set it was captured
+// with: replays of one graph must not overlap).
+constexpr int kDealSets = 64;
+constexpr int kDealStride = 256;  // ints per set: XCD x's counter at 16 x, the exits at 128
+__device__ __align__(256) int g_w512_deal[kDealSets * kDealStride];
+
 template <int MT, int NTW, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   constexpr int BKS = 32;          // k per stage
@@ -388,7 +406,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   const int nbx = has_x ? (p.x_rows + MT - 1) / MT : 0;
   const int items_x = nbx * num_n;
   const int per_xcd_x = (items_x + 7) / 8;
-  const int span = (per_xcd + per_xcd_x) * 8;
+  int* const deal = g_w512_deal + p.deal_set * kDealStride;
+  const int wg_xcd = gridDim.x / 8;  // workgroups per XCD (the launcher rounds to 8)
+  int xcd = blockIdx.x % 8;  // the XCD whose items this workgroup takes: its own first
+  int tried = 1;
 
   // fragment reads: lane (l32, h) reads logical chunk 2 ks + h of row base + l32 (base % 32 == 0)
   const int rd0 = l32 * BKS + (((0 + h) ^ ((l32 >> 2) & 3)) * 8);
@@ -397,15 +418,37 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   const int dr = lane >> 2;
   const int dc = (lane & 3) ^ ((dr >> 2) & 3);  // the logical chunk that lands in that slot
   const uint32_t ring_base = lds_addr(ring);
+  // the next item's index passes from wave 0 to the others through the first word of the
+  // ring buffer of the last stage: no load issued past the last stage lands there, and
+  // every wave has read that stage's fragments before the stage's barrier
+  int* const slot = reinterpret_cast<int*>(ring + ((nk - 1) % NSTAGE) * SELEM);
+  auto fetch_now = [&]() {  // the next index of XCD xcd's items, for the whole workgroup
+    if (tid == 0)
+      *slot = __hip_atomic_fetch_add(deal + xcd * 16, 1, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const int k = __builtin_amdgcn_readfirstlane(wg_xcd + *slot);
+    __syncthreads();  // every wave has it before the slot is written again
+    return k;
+  };
 
-  for (int it = blockIdx.x; it < span; it += gridDim.x) {
-    const int xi = it / 8 - per_xcd;  // >= 0: an item of the extra expert
-    const bool xs = xi >= 0;
+  for (int k = blockIdx.x / 8;;) {
+    // item k of XCD xcd: its routed items first (L = xcd * per_xcd + k), then the extra
+    // expert's (Lx = xcd * per_xcd_x + k - n_r)
+    const int n_r = max(0, min(per_xcd, items - xcd * per_xcd));
+    const int n_local = n_r + max(0, min(per_xcd_x, items_x - xcd * per_xcd_x));
+    if (k >= n_local) {  // that XCD's items are all taken: take the next XCD's
+      if (tried == 8) break;
+      ++tried;
+      xcd = (xcd + 1) % 8;
+      k = fetch_now();
+      continue;
+    }
+    const bool xs = k >= n_r;
     int pid_n, row0, e;
     bool w_once;  // the W tile is streamed by this item only: non-temporal loads
     if (!xs) {
-      const int L = (it % 8) * per_xcd + it / 8;
-      if (L >= items) continue;
+      const int L = xcd * per_xcd + k;
       // expert-aligned order (as moe_gemm_dma_kernel): column tile major, row block fastest
       const int b = L / num_n;
       const int eb = p.eids[b];
@@ -418,11 +461,13 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       pid_n = local / cnt;
       const int pid_m = mb + local % cnt;
       row0 = pid_m * MT;
-      if (p.sti[row0] >= p.num_valid) continue;
+      if (p.sti[row0] >= p.num_valid) {  // a block with no real row: nothing to compute
+        k = fetch_now();
+        continue;
+      }
       e = p.eids[pid_m];
     } else {
-      const int Lx = (it % 8) * per_xcd_x + xi;
-      if (Lx >= items_x) continue;
+      const int Lx = xcd * per_xcd_x + (k - n_r);
       pid_n = Lx / nbx;
       row0 = (Lx % nbx) * MT;
       e = 0;
@@ -645,6 +690,20 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       }
       }
     };
+    // the next item's index, fetched while this one runs.  The token-row offsets are
+    // complete first: a load the compiler still counts as pending where the branch joins
+    // would make it wait for the fetch there.  The address goes through a register the
+    // compiler cannot prove uniform, or the atomic becomes a wave reduction that waits for
+    // its result at once.  The first wait of the ring (an explicit vmcnt) covers it.
+#pragma unroll
+    for (int i = 0; i < AI; ++i) asm volatile("" : : "v"(avoff[i]) : "memory");
+    int fetched = 0;
+    if (tid == 0) {
+      int z;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+      fetched = __hip_atomic_fetch_add(deal + xcd * 16 + z, 1, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+    }
     switch (nvf) {
       case 0: run(std::integral_constant<int, 0>{}); break;
       case 1: run(std::integral_constant<int, 1>{}); break;
@@ -652,13 +711,26 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       case 3: run(std::integral_constant<int, (TF >= 3 ? 3 : 1)>{}); break;
       default: run(std::integral_constant<int, (TF >= 4 ? 4 : 1)>{}); break;
     }
+    if (tid == 0) *slot = fetched;
     __syncthreads();  // the ring is refilled by the next item
+    k = __builtin_amdgcn_readfirstlane(wg_xcd + *slot);
+    __syncthreads();  // every wave has the index before the next prologue refills the ring
+  }
+  // the last workgroup out clears the set for the next launch that uses it
+  if (tid == 0 && __hip_atomic_fetch_add(deal + 128, 1, __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
+    for (int x = 0; x < 8; ++x)
+      __hip_atomic_store(deal + x * 16, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(deal + 128, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 template <int MT, int NTW, bool GATED, bool WEIGHTED>
-int launch_w512(const GemmArgs& a, int capacity, hipStream_t st) {
+int launch_w512(const GemmArgs& a_in, int capacity, hipStream_t st) {
   constexpr int NO = GATED ? NTW / 2 : NTW;
+  static std::atomic<unsigned> next_set{0};
+  GemmArgs a = a_in;
+  a.deal_set = (int)(next_set.fetch_add(1, std::memory_order_relaxed) % kDealSets);
   if ((a.n_out % (GATED ? 256 : 512)) || (a.K % 64)) return GLM52_EUNSUPPORTED;
   const int x_blocks = (a.Wp && a.Wx && a.x_rows > 0) ? (a.x_rows + MT - 1) / MT : 0;
   const int items_max = (capacity / MT + x_blocks) * (a.n_out / NO);

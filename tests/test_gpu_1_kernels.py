@@ -575,6 +575,71 @@ def test_moe_gemm_packed_shared_matches_separate_launches(gpu, bm, T):
            "shared w13 (fp32 reference)")
 
 
+@pytest.mark.parametrize("bm", [64, 128, 256])
+def test_w512_item_dealing(gpu, bm):
+    """The prefill tile deals its items from per-XCD counters that the last workgroup out
+    clears, one counter set per launch out of 64 in turn.  (1) A layout block with no real
+    row (the workgroup fetches the next item at once) leaves the results as they are
+    without it.  (2) 70 launches in a row (more than the 64 sets, so every set is reused
+    after it was cleared) all give the first launch's bits.  (3) Two launches issued on two
+    streams at once give the bits of the same launches in order."""
+    say(f"w512 item dealing bm={bm}")
+    T, E, H, I, k = 300, 8, 512, 256, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 700 + bm, gpu)
+    ag = a.to(gpu)
+    w13p, w2p = KG.pack_w512(w13.to(gpu), I, I, True), KG.pack_w512(w2.to(gpu), H, 0, False)
+    twf = tw.reshape(-1).contiguous().to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), bm, E)
+    cfg = {"BLOCK_M": bm}
+    R = T * k
+    nan = float("nan")
+
+    def gateup(layout, out):
+        KG.moe_gemm_packed(ag, k, w13p, out, None, *layout, R, I, True, cfg)
+
+    def down(layout, x, out):
+        KG.moe_gemm_packed(x, 1, w2p, out, twf, *layout, R, H, False, cfg)
+
+    act = torch.full((R, I), nan, dtype=BF16, device=gpu)
+    gateup((sti, eids, ntp), act)
+    y = torch.full((R, H), nan, dtype=BF16, device=gpu)
+    down((sti, eids, ntp), act, y)
+    torch.cuda.synchronize()
+    _close(y, _down_ref(act, w2, ids, tw), "w2 weighted")
+
+    # (1) an all-padding block (sentinel rows) inside the run of the middle block's expert
+    n = int(ntp.item())
+    nb, b = n // bm, n // bm // 2
+    s, e_ = sti.cpu(), eids.cpu()
+    sti2 = torch.cat([s[: b * bm], torch.full((bm,), R, dtype=torch.int32), s[b * bm: n]])
+    eids2 = torch.cat([e_[:b], e_[b: b + 1], e_[b:nb]])
+    lay2 = (sti2.to(gpu), eids2.to(gpu), torch.tensor([n + bm], dtype=torch.int32, device=gpu))
+    act2 = torch.full_like(act, nan)
+    gateup(lay2, act2)
+    y2 = torch.full_like(y, nan)
+    down(lay2, act2, y2)
+    torch.cuda.synchronize()
+    assert torch.equal(act2, act) and torch.equal(y2, y)
+
+    # (2) launches in a row, every output refilled first
+    y3 = torch.empty_like(y)
+    for i in range(70):
+        y3.fill_(nan)
+        down((sti, eids, ntp), act, y3)
+        assert torch.equal(y3, y), f"launch {i}"
+
+    # (3) two streams at once (default priority)
+    act4, y4 = torch.full_like(act, nan), torch.full_like(y, nan)
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(s1):
+        gateup((sti, eids, ntp), act4)
+    with torch.cuda.stream(s2):
+        down((sti, eids, ntp), act, y4)
+    torch.cuda.synchronize()
+    assert torch.equal(act4, act) and torch.equal(y4, y)
+
+
 @pytest.mark.parametrize("T", [1, 3, 16, 40])
 def test_packed_weight_stream_matches_in_place(gpu, T):
     """The decode weight stream (block size 16) on packed weights, routed and shared expert
