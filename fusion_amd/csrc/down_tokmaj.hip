@@ -116,11 +116,11 @@ __global__ __launch_bounds__(256) void down_tokmaj_kernel(
 
 // The same sum on packed weights (glm52_pack_w512 of w2 for N plain outputs).  The 16 rows
 // of packed load slot q of 512-row tile P are rows P * 512 + (q / 8) * 128 + (q % 8 / 2) * 32
-// + (q % 2) * 8 + phi32(p), p = 0 .. 15; the slot holds their K / 32 stages one after the
-// other, 1 KB each, lane l's 16 bytes holding row p = l / 4, 8-k chunk (l % 4) ^ (p / 4 % 4).
-// Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token t: wave w takes the
-// pieces of QS stages (QS KB of contiguous memory) that start at stages QS w and QS (4 + w),
-// so the four waves read one 4 QS KB run at a time; every load reads one stage's whole 1 KB,
+// + (q % 2) * 8 + phi32(p), p = 0 .. 15; the slot holds their K / 32 stages of 1 KB each,
+// kPackStride apart (packed_slot_off), lane l's 16 bytes holding row p = l / 4, 8-k chunk
+// (l % 4) ^ (p / 4 % 4).  Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token
+// t: wave w takes the pieces of QS stages that start at stages QS w and QS (4 + w), so the
+// four waves read 4 QS stages of the slot at a time; every load reads one stage's whole 1 KB,
 // and a lane keeps one fp32 partial of its row over all pieces.  The 4 lanes of a row, then the 4 waves, meet in a fixed order.  The pieces flow
 // through two register buffers, so a wave has two pieces' loads in flight; four waves per
 // workgroup let two workgroups share a CU (about 210 VGPRs), so at T = 1 and N = 6144 the
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
   const int num_n512 = N / 512;
   const int pr = lane >> 2;                      // the lane's row in the slot
   const int kc = (lane & 3) ^ ((pr >> 2) & 3);   // and its 8-k chunk of every stage
-  const int64_t toff = P * packed_tile_elems(NK) + q * packed_slot_elems(NK) + lane * 8;
+  const int64_t toff = P * packed_tile_elems(NK) + packed_slot_off(NK, q) + lane * 8;
   const int npieces = 2 * (topk + (w2sp ? 1 : 0));
 
   // piece c: half c % 2 of the wave's stages of unit c / 2 -- routed expert u of the
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
       ar[i] = arow ? ldg(arow + (kt0 + i) * 32 + kc * 8) : make_uint4(0, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < QS; ++i)
-      wr[i] = wb ? ldg_nt(wb + (kt0 + i) * 512) : make_uint4(0, 0, 0, 0);
+      wr[i] = wb ? ldg_nt(wb + (int64_t)(kt0 + i) * kPackStride) : make_uint4(0, 0, 0, 0);
   };
 
   float acc = 0.f;

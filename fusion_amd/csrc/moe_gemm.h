@@ -90,12 +90,23 @@ GLM52_DEV uint32_t lds_addr(const uint16_t* p) {
 // The packed weight layout (glm52_pack_w512).  W row (inside its 32-row group) held at
 // LDS row p of the 512-row tile; load slot w * 8 + i of a tile holds 16 rows of one 32-row
 // group (rows phi32(p) + 8 (i % 2) for p = 0 .. 15), each 32-k stage of them as 1 KB, lane
-// l's 16 bytes being row p = l / 4, 8-k chunk (l % 4) ^ ((p / 4) % 4); a slot's nk = K / 32
-// stages follow each other (nk KB per slot), and a tile's 32 slots likewise.
+// l's 16 bytes being row p = l / 4, 8-k chunk (l % 4) ^ ((p / 4) % 4).  A tile's 32 slots
+// (nk = K / 32 stages each) are interleaved 1 KB at a time in groups of kPackG = 8: stage j
+// of slot s sits at KB (s / 8) * 8 nk + 8 j + s % 8 of the tile.  A slot's stages are 8 KB
+// apart, as a row-major W's 1 KB row runs are a row stride apart, which the decode weight
+// stream reads faster than one contiguous run (T = 256: w13 2224 -> 2081 us, w2 1380 ->
+// 1319 us; interleaving 16 slots measured the same); a 512-row tile's stage is four 8 KB
+// runs.
 GLM52_DEV int phi32(int p) { return ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); }
 // elements of one packed slot and of one packed 512-row tile, for nk 32-k stages
 __host__ __device__ inline int64_t packed_slot_elems(int nk) { return (int64_t)nk * 512; }
 __host__ __device__ inline int64_t packed_tile_elems(int nk) { return 32 * packed_slot_elems(nk); }
+// stage j of slot s sits at element packed_slot_off(nk, s) + j * kPackStride of its tile
+constexpr int kPackG = 8;
+constexpr int kPackStride = kPackG * 512;  // elements between a slot's successive stages
+__host__ __device__ inline int64_t packed_slot_off(int nk, int s) {
+  return ((int64_t)(s / kPackG) * nk * kPackG + s % kPackG) * 512;
+}
 
 struct GemmArgs {
   const uint16_t* A;

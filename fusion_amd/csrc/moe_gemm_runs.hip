@@ -244,19 +244,20 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     if constexpr (PACKED) {
       // item n of the layout block: load slot ps of packed tile P (gated: half hs of the
       // `gate` slot and the same half of its `up` slot, four slots on, 512 B each); wave
-      // instruction i loads 32-k stage 16 s + 4 wv + i of the slot(s) for 512-k stage s, so
-      // an item streams its slot's K / 32 KB as one contiguous run
+      // instruction i loads 32-k stage 16 s + 4 wv + i of the slot(s) for 512-k stage s: an
+      // item streams its slot's K / 32 pieces of 1 KB, kPackStride apart
       const int n = L % num_n;
       const int P = n >> 5, q5 = n & 31;
       const int ps = GATED ? (q5 >> 3) * 8 + ((q5 >> 1) & 3) : q5;
       const uint16_t* tb = uniform_ptr(extra ? pw_x : pw_r) +
                            ((int64_t)e * num_n512 + P) * packed_tile_elems(nk32) +
-                           ps * packed_slot_elems(nk32);
-      dw[0] = tb + (int64_t)(wvu * 4) * 512;  // the slot's 32-k stages follow 1 KB apart
+                           packed_slot_off(nk32, ps);
+      dw[0] = tb + (int64_t)(wvu * 4) * kPackStride;  // the slot's 32-k stages
       if (GATED) {
         const int hs = q5 & 1;
         wvo = (uint32_t)(lane < 32 ? (hs * 32 + lane) * 16
-                                   : 4 * packed_slot_elems(nk32) * 2 + (hs * 32 + lane - 32) * 16);
+                                   : (packed_slot_off(nk32, ps + 4) - packed_slot_off(nk32, ps)) * 2 +
+                                         (hs * 32 + lane - 32) * 16);
       } else {
         wvo = (uint32_t)(lane * 16);
       }
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     for (int i = 0; i < 4; ++i) {
       const int R = wvu * 4 + i;
       if constexpr (PACKED)
-        dma16s_nt(uniform_ptr(dw[0] + (int64_t)(s * 16 + i) * 512), wvo,
+        dma16s_nt(uniform_ptr(dw[0] + (int64_t)(s * 16 + i) * kPackStride), wvo,
                   sb + (uint32_t)(R * KS * 2));
       else
         dma16s_nt(dw[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));

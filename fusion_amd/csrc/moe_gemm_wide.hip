@@ -322,11 +322,11 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 namespace {
 
 // Packed W (PACKED): expert e's 512-row tiles P follow each other; inside a tile its 32 load
-// slots (slot w * 8 + i: what load instruction i of wave w fetches), nk KB each; inside a
-// slot its nk stages, 1 KB each, lane l's 16 bytes at l * 16: exactly
-// what the instruction writes to LDS.  Every load reads 1 KB of contiguous memory, and a
-// slot's successive stages are adjacent, which the decode weight stream (one slot per item)
-// reads as one contiguous run.
+// slots (slot w * 8 + i: what load instruction i of wave w fetches), nk stages of 1 KB each,
+// lane l's 16 bytes at l * 16: exactly what the instruction writes to LDS.  The slots are
+// interleaved a stage at a time in groups of 8 (packed_slot_off): every load reads 1 KB of
+// contiguous memory, a stage of the tile is four 8 KB runs, and the decode weight stream
+// (one slot per item) reads a slot's stages 8 KB apart.
 
 // W row (relative to the tile's first `gate` row, or to n0) and k chunk of packed lane l of
 // load instruction i of wave w: the row and chunk the unpacked loads of that slot fetch.
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     for (int i = 0; i < WI; ++i) {
       if (PACKED) {
         // load slot sub * 32 / SPLIT + wv * WI + i of the 512-row tile: nk KB per slot
-        wvoff[i] = (uint32_t)((sub * (32 / SPLIT) + wv * WI + i) * packed_slot_elems(nk) * 2 +
+        wvoff[i] = (uint32_t)(packed_slot_off(nk, sub * (32 / SPLIT) + wv * WI + i) * 2 +
                               lane * 16);
       } else {
         const int slab = sub * (NTW / RPI) + wv * WI + i;  // 1 KB slab of the 512-row tile
@@ -527,7 +527,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       const int kc = min(kt, nk - 1) * BKS;
       const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
-        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * 512 : wexp + kc;
+        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * kPackStride : wexp + kc;
         const uint32_t vo = past ? 0u : wvoff[i];
         if (w_once)
           dma16s_nt(src, vo, sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
@@ -783,7 +783,7 @@ int launch_w512_bm(const GemmArgs& a, int capacity, hipStream_t st) {
 
 // One 16-byte chunk of the packed layout per thread and step: chunk d is lane d % 64 of
 // stage (d / 64) % nk of load slot (d / (64 nk)) % 32 of tile d / (2048 nk), written at
-// stage KB (+ 16 lane bytes) of that slot, the slots nk KB apart.
+// packed_slot_off(nk, slot) + stage * kPackStride (+ 16 lane bytes) of its tile.
 template <bool GATED>
 __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restrict__ w,
                                                         int64_t swe, int64_t swn, int64_t swk,
@@ -799,7 +799,8 @@ __global__ __launch_bounds__(256) void pack_w512_kernel(const uint16_t* __restri
     const int64_t rest = q / nk;  // tile * 32 + slot
     const int slot = (int)(rest % 32);
     const int64_t tile = rest / 32;
-    uint16_t* dst = out + rest * packed_slot_elems(nk) + kt * 512 + l * 8;
+    uint16_t* dst = out + tile * packed_tile_elems(nk) + packed_slot_off(nk, slot) +
+                    (int64_t)kt * kPackStride + l * 8;
     const int pid_n = (int)(tile % num_n);
     const int64_t e = tile / num_n;
     const int row = pid_n * NO + w512_row(GATED, gu_off, slot / 8, slot % 8, l);
