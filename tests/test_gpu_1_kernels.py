@@ -99,8 +99,8 @@ def test_add_rmsnorm_strided_rows(gpu):
 
 # ------------------------------------------------------------------ router
 @pytest.mark.parametrize("T,bias", [(1, "normal"), (3, "normal"), (8, "zipf"), (13, "zipf"),
-                                    (32, "normal"), (100, "zero"), (2048, "normal"),
-                                    (2048, "zipf")])
+                                    (32, "normal"), (100, "zero"), (256, "normal"),
+                                    (2048, "normal"), (2048, "zipf")])
 def test_router_bitwise(gpu, T, bias):
     say(f"router T={T} bias={bias}")
     fe = front_end(T, bias=bias)
