@@ -15,6 +15,12 @@
 // `v_mfma_f32_16x16x32_bf16` (W rows x tokens) and the partial sums meet in LDS in a fixed
 // order at the item's end.
 //
+// Paired slots (plain launch on packed weights, K >= 1024): an item is two adjacent
+// packed slots, 32 W rows (32 outputs), against the same token rows; a stage carries 32 KB
+// of W per 16 KB of token rows instead of 16 KB, through a ring of three buffers with two
+// in flight.  At T = 256 the w2 launch runs 1168 against 1310 us (T = 64: 903 against
+// 1007 us), the same bits.
+//
 // Pipeline.  A stage is the 512-k run of the item's 16 W rows and its real token rows (up
 // to 16; the rows of padding slots are not loaded, and whatever their LDS rows hold only
 // reaches the discarded outputs of those slots).  Stages flow through a ring of four LDS
@@ -161,10 +167,21 @@ GLM52_DEV void wait_vmcnt_at_most(int n) {
   }
 }
 
-template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED>
+// PAIR (plain, packed, not routing): an item is two adjacent packed slots (32 W rows, 32
+// outputs) against the same token rows, so a stage carries twice the W bytes per token
+// row; a ring of three 48 KB stages, two in flight.  At T = 256 the token-row loads are a
+// sixth of the w2 launch (1314 against 1105 us without them, a timing-only copy).  One
+// partial-sum buffer: an item's stash and the previous item's reduce are a barrier apart
+// when an item has two or more stages (the launcher requires K >= 1024).
+template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED, bool PAIR = false>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(1024))) uint16_t ring[NSTAGE * SELEM];
-  __shared__ float red[2][4][4][kWave];  // partial sums of the last two items, by wave
+  static_assert(!PAIR || (PACKED && !GATED && !ROUTE), "paired slots: plain packed only");
+  constexpr int NSB = PAIR ? 3 : NSTAGE;  // ring buffers
+  constexpr int WR = PAIR ? 32 : 16;      // W rows (1 KB slabs) of a stage; token rows follow
+  constexpr int SE = (WR + 16) * KS;      // elements per stage
+  constexpr int NB = PAIR ? 2 : 1;        // 16 x 16 output blocks per item
+  __shared__ __attribute__((aligned(1024))) uint16_t ring[NSB * SE];
+  __shared__ float red[PAIR ? 1 : 2][4][4 * NB][kWave];  // partial sums by wave
   __shared__ int meta_tok[NMETA][16];    // flat ids of an item's token rows
   __shared__ float meta_w[NMETA][16];    // their routing weights (weighted)
   __shared__ RouteLds rs;
@@ -175,7 +192,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   const int wvu = __builtin_amdgcn_readfirstlane(wv);
   const int r16 = lane % 16, g = lane / 16;
 
-  constexpr int NOC = GATED ? 8 : 16;  // outputs per item
+  constexpr int NOC = GATED ? 8 : 16 * NB;  // outputs per item
   const int xm = (p.x_rows + 15) / 16;
   const int num_n = p.n_out / NOC;
   const int x_items = xm * num_n;  // the extra expert's items come first
@@ -246,13 +263,15 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       // `gate` slot and the same half of its `up` slot, four slots on, 512 B each); wave
       // instruction i loads 32-k stage 16 s + 4 wv + i of the slot(s) for 512-k stage s: an
       // item streams its slot's K / 32 pieces of 1 KB, kPackStride apart
-      const int n = L % num_n;
+      const int n = PAIR ? 2 * (L % num_n) : L % num_n;  // paired: the first slot's item
       const int P = n >> 5, q5 = n & 31;
       const int ps = GATED ? (q5 >> 3) * 8 + ((q5 >> 1) & 3) : q5;
       const uint16_t* tb = uniform_ptr(extra ? pw_x : pw_r) +
                            ((int64_t)e * num_n512 + P) * packed_tile_elems(nk32) +
                            packed_slot_off(nk32, ps);
       dw[0] = tb + (int64_t)(wvu * 4) * kPackStride;  // the slot's 32-k stages
+      if (PAIR)  // the second slot's stages
+        dw[1] = dw[0] + (packed_slot_off(nk32, ps + 1) - packed_slot_off(nk32, ps));
       if (GATED) {
         const int hs = q5 & 1;
         wvo = (uint32_t)(lane < 32 ? (hs * 32 + lane) * 16
@@ -307,19 +326,21 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     }
   };
   auto issue = [&](int s, int buf) {  // stage s (512-k run) of the item being loaded
-    const uint32_t sb = ring_base + (uint32_t)(buf * SELEM * 2);
+    const uint32_t sb = ring_base + (uint32_t)(buf * SE * 2);
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int R = b * 16 + wvu * 4 + i;
+        if constexpr (PACKED)
+          dma16s_nt(uniform_ptr(dw[b] + (int64_t)(s * 16 + i) * kPackStride), wvo,
+                    sb + (uint32_t)(R * KS * 2));
+        else
+          dma16s_nt(dw[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
+      }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int R = wvu * 4 + i;
-      if constexpr (PACKED)
-        dma16s_nt(uniform_ptr(dw[0] + (int64_t)(s * 16 + i) * kPackStride), wvo,
-                  sb + (uint32_t)(R * KS * 2));
-      else
-        dma16s_nt(dw[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int R = 16 + wvu * 4 + i;
+      const int R = WR + wvu * 4 + i;
       if (i < da_n) {
         if constexpr (PACKED)  // a per-lane address: SGPRs are short in these instances
           dma16(da[i] + s * KS + (lane ^ (R & 15)) * 8, sb + (uint32_t)(R * KS * 2));
@@ -327,7 +348,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
           dma16s(da[i] + s * KS, (uint32_t)((lane ^ (R & 15)) * 16), sb + (uint32_t)(R * KS * 2));
       }
     }
-    return 4 + da_n;  // loads issued
+    return 4 * NB + da_n;  // loads issued
   };
   int d_item = blockIdx.x, d_s = 0;
   auto dma_advance = [&]() {
@@ -509,17 +530,20 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       return (4 * r16 + (g ^ ((r16 >> 2) & 3))) * 8;
     }
   };
-  auto compute = [&](int buf, floatx4_t acc, int wofs) {
-    const uint16_t* sb = ring + buf * SELEM;
+  auto compute = [&](int buf, floatx4_t (&acc)[NB], int wofs) {
+    const uint16_t* sb = ring + buf * SE;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int c = (wv * 4 + q) * 4 + g;  // logical 16-byte chunk of the 512-k run
-      const uint4 wf = PACKED ? *reinterpret_cast<const uint4*>(sb + (wv * 4 + q) * 512 + wofs)
-                              : *reinterpret_cast<const uint4*>(sb + r16 * KS + ((c ^ r16) * 8));
-      const uint4 af = *reinterpret_cast<const uint4*>(sb + (16 + r16) * KS + ((c ^ r16) * 8));
-      acc = mfma16(wf, af, acc);  // C[W row 4 g + i][token r16]
+      const uint4 af = *reinterpret_cast<const uint4*>(sb + (WR + r16) * KS + ((c ^ r16) * 8));
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {  // block b: the item's slot b (paired) or its only one
+        const uint4 wf =
+            PACKED ? *reinterpret_cast<const uint4*>(sb + (b * 16 + wv * 4 + q) * 512 + wofs)
+                   : *reinterpret_cast<const uint4*>(sb + r16 * KS + ((c ^ r16) * 8));
+        acc[b] = mfma16(wf, af, acc[b]);  // C[W row 4 g + i][token r16]
+      }
     }
-    return acc;
   };
   // Epilogue, in two halves.  At an item's last stage every wave stashes its partial sums
   // (no barrier).  After the next stage's barrier all four waves finish it together: wave
@@ -527,18 +551,21 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // waves' partials in a fixed order and stores; the 16 lanes of a token write 16
   // consecutive outputs.  A partial for W row r and token c sits in register r % 4 of
   // lane (r / 4) * 16 + c.
-  auto stash = [&](int par, floatx4_t acc) {
+  auto stash = [&](int par, const floatx4_t (&acc)[NB]) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[par][wv][i][lane] = acc[i];
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[PAIR ? 0 : par][wv][b * 4 + i][lane] = acc[b][i];
   };
-  auto rsum = [&](int par, int row, int c) {
-    const int i = row % 4, l = (row / 4) * 16 + c;
-    return ((red[par][0][i][l] + red[par][1][i][l]) + red[par][2][i][l]) + red[par][3][i][l];
+  auto rsum = [&](int par, int b, int row, int c) {
+    const int i = b * 4 + row % 4, l = (row / 4) * 16 + c;
+    const auto& rd = red[PAIR ? 0 : par];
+    return ((rd[0][i][l] + rd[1][i][l]) + rd[2][i][l]) + rd[3][i][l];
   };
   // output column of output j of item L: n0 + j, or packed, row phi32(p) of the slot's
   // 32-row group (gated p = 8 hs + j)
-  auto out_col = [&](int L, int j) {
-    const int n = L % num_n;
+  auto out_col = [&](int L, int b, int j) {
+    const int n = PAIR ? 2 * (L % num_n) + b : L % num_n;
     if constexpr (!PACKED) {
       return n * NOC + j;
     } else if constexpr (GATED) {
@@ -557,28 +584,35 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     const bool extra = m < xm;
     const int slot = (it / (int)gridDim.x) % NMETA;
     const int c = wv * 4 + lane / 16;  // token column of the slice
-    const int j = lane % 16;           // output of the item
+    const int j = lane % 16;           // output of the item's block
     if (!GATED && p.merge_topk > 0) {  // atomic merge: lane pairs (j, j + 1) add as one word
       const int tok = meta_tok[slot][c];
-      float v = rsum(par, j, c);
-      if (WEIGHTED && !extra) v = v * meta_w[slot][c];
-      const float v1 = __shfl_down(v, 1, 16);  // every lane is active here
-      if (tok < 0 || (j & 1) || extra) return;
-      atomic_add_bf16x2(p.C + (int64_t)(tok / p.merge_topk) * p.scm + out_col(L, j), v, v1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        float v = rsum(par, b, j, c);
+        if (WEIGHTED && !extra) v = v * meta_w[slot][c];
+        const float v1 = __shfl_down(v, 1, 16);  // every lane is active here
+        if (tok >= 0 && !(j & 1) && !extra)
+          atomic_add_bf16x2(p.C + (int64_t)(tok / p.merge_topk) * p.scm + out_col(L, b, j), v,
+                            v1);
+      }
       return;
     }
     if (GATED && j >= 8) return;
     const int tok = meta_tok[slot][c];
     if (tok < 0) return;
-    float v;
-    if (GATED) {
-      v = silu_mul(rsum(par, j, c), rsum(par, 8 + j, c));  // `gate` row j, `up` row 8 + j
-    } else {
-      v = rsum(par, j, c);
-      if (WEIGHTED && !extra) v = v * meta_w[slot][c];
-    }
     uint16_t* dst = extra ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm;
-    dst[out_col(L, j)] = f32_to_bf16(v);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      float v;
+      if (GATED) {
+        v = silu_mul(rsum(par, 0, j, c), rsum(par, 0, 8 + j, c));  // `gate` row j, `up` 8 + j
+      } else {
+        v = rsum(par, b, j, c);
+        if (WEIGHTED && !extra) v = v * meta_w[slot][c];
+      }
+      dst[out_col(L, b, j)] = f32_to_bf16(v);
+    }
   };
 
   // prologue: the first three stages.  In routing mode the logits are loaded first and a
@@ -598,7 +632,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   if (!ROUTE) {
     if ((int)blockIdx.x >= items) return;
     dma_setup(d_item);
-    prologue_to(3);
+    prologue_to(NSB - 1);
     dma_advance();
   } else {
     route_load();
@@ -629,29 +663,38 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   int n1 = nst[1], n2 = nst[2];
   const int total = ((items - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x) * nks;
 
-  floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+  floatx4_t acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   int c_item = blockIdx.x, c_s = 0;
   int wofs = w_ofs(c_item);
   int pend = -1, par = 0;  // the item whose partial sums wait in red[par ^ 1], if any
 #pragma unroll 1
   for (int j = 0; j < total; ++j) {
-    // stage j landed for this wave (stages j+1, j+2 may be in flight) and for every wave;
+    // stage j landed for this wave (the newer stages may be in flight) and for every wave;
     // every wave is done with the buffer refilled next, and the stashed partials are visible
-    wait_vmcnt_at_most(n1 + n2);
-    __syncthreads();
-    n1 = n2;
-    n2 = issue(d_s, (j + NSTAGE - 1) % NSTAGE);
+    if constexpr (PAIR) {
+      wait_vmcnt_at_most(n1);  // stage j + 1 in flight
+      __syncthreads();
+      n1 = issue(d_s, (j + NSB - 1) % NSB);
+    } else {
+      wait_vmcnt_at_most(n1 + n2);  // stages j + 1, j + 2 in flight
+      __syncthreads();
+      n1 = n2;
+      n2 = issue(d_s, (j + NSB - 1) % NSB);
+    }
     dma_advance();
     if (pend >= 0) {
       finish(pend, par ^ 1);
       pend = -1;
     }
-    acc = compute(j % NSTAGE, acc, wofs);
+    compute(j % NSB, acc, wofs);
     if (++c_s == nks) {
       stash(par, acc);
       pend = c_item;
       par ^= 1;
-      acc = floatx4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int b = 0; b < NB; ++b) acc[b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
       c_s = 0;
       c_item += gridDim.x;
       wofs = w_ofs(c_item);
@@ -664,10 +707,11 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   GLM52_WAIT_VMCNT(0);  // the re-reads past the last stage land before the workgroup ends
 }
 
-template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED>
+template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED, bool PAIR = false>
 int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
-  constexpr int NOC = GATED ? 8 : 16;
-  if (a.BM != 16 || (a.n_out % NOC) || (a.K % KS) || a.K / KS < 1) return GLM52_EUNSUPPORTED;
+  constexpr int NOC = GATED ? 8 : (PAIR ? 32 : 16);
+  if (a.BM != 16 || (a.n_out % NOC) || (a.K % KS) || a.K / KS < (PAIR ? 2 : 1))
+    return GLM52_EUNSUPPORTED;
   // packed: whole 512-row tiles (256 outputs gated), no atomic merge
   if (PACKED && ((a.n_out % (GATED ? 256 : 512)) || a.merge_topk > 0 ||
                  (a.x_rows > 0 && !a.Wx)))
@@ -679,7 +723,7 @@ int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
   const int items_max = (capacity / 16 + (a.x_rows + 15) / 16) * (a.n_out / NOC);
   int grid = items_max < 256 ? items_max : 256;
   if (grid < 1) grid = 1;
-  moe_gemm_runs_kernel<GATED, WEIGHTED, ROUTE, PACKED><<<grid, 256, 0, st>>>(a);
+  moe_gemm_runs_kernel<GATED, WEIGHTED, ROUTE, PACKED, PAIR><<<grid, 256, 0, st>>>(a);
   GLM52_RETURN_LAUNCH();
 }
 
@@ -694,6 +738,10 @@ int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, bool
       return launch_runs_t<true, false, true, true>(a, capacity, st);
     }
     if (gated) return weighted ? launch_runs_t<true, true, false, true>(a, capacity, st) : launch_runs_t<true, false, false, true>(a, capacity, st);
+    // plain: paired slots from two 512-k stages on (K >= 1024)
+    if (a.K >= 2 * KS)
+      return weighted ? launch_runs_t<false, true, false, true, true>(a, capacity, st)
+                      : launch_runs_t<false, false, false, true, true>(a, capacity, st);
     return weighted ? launch_runs_t<false, true, false, true>(a, capacity, st) : launch_runs_t<false, false, false, true>(a, capacity, st);
   }
   if (route) {
