@@ -15,11 +15,13 @@
 // `v_mfma_f32_16x16x32_bf16` (W rows x tokens) and the partial sums meet in LDS in a fixed
 // order at the item's end.
 //
-// Paired slots (plain launch on packed weights, K >= 1024): an item is two adjacent
-// packed slots, 32 W rows (32 outputs), against the same token rows; a stage carries 32 KB
-// of W per 16 KB of token rows instead of 16 KB, through a ring of three buffers with two
-// in flight.  At T = 256 the w2 launch runs 1168 against 1310 us (T = 64: 903 against
-// 1007 us), the same bits.
+// Paired slots (packed weights, K >= 1024; the gated launch from 1024 routed rows): an
+// item is two packed slots against the same token rows -- plain: two adjacent slots, 32 W
+// rows (32 outputs); gated: both halves of a `gate` slot and of its `up` slot (2 x 8
+// outputs) -- so a stage carries 32 KB of W per 16 KB of token rows instead of 16 KB,
+// through a ring of three buffers with two in flight.  At T = 256 the w2 launch runs 1168
+// against 1310 us (T = 64: 903 against 1007 us) and the w13 launch 1985 against 2086 us,
+// the same bits.
 //
 // Pipeline.  A stage is the 512-k run of the item's 16 W rows and its real token rows (up
 // to 16; the rows of padding slots are not loaded, and whatever their LDS rows hold only
@@ -167,15 +169,16 @@ GLM52_DEV void wait_vmcnt_at_most(int n) {
   }
 }
 
-// PAIR (plain, packed, not routing): an item is two adjacent packed slots (32 W rows, 32
-// outputs) against the same token rows, so a stage carries twice the W bytes per token
+// PAIR (packed, not routing): an item is two packed slots against the same token rows --
+// plain: two adjacent slots (32 W rows, 32 outputs); gated: a whole `gate` slot and its
+// `up` slot (both halves, 2 x 8 outputs) -- so a stage carries twice the W bytes per token
 // row; a ring of three 48 KB stages, two in flight.  At T = 256 the token-row loads are a
 // sixth of the w2 launch (1314 against 1105 us without them, a timing-only copy).  One
 // partial-sum buffer: an item's stash and the previous item's reduce are a barrier apart
 // when an item has two or more stages (the launcher requires K >= 1024).
 template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED, bool PAIR = false>
 __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
-  static_assert(!PAIR || (PACKED && !GATED && !ROUTE), "paired slots: plain packed only");
+  static_assert(!PAIR || (PACKED && !ROUTE), "paired slots: packed, not routing");
   constexpr int NSB = PAIR ? 3 : NSTAGE;  // ring buffers
   constexpr int WR = PAIR ? 32 : 16;      // W rows (1 KB slabs) of a stage; token rows follow
   constexpr int SE = (WR + 16) * KS;      // elements per stage
@@ -192,7 +195,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   const int wvu = __builtin_amdgcn_readfirstlane(wv);
   const int r16 = lane % 16, g = lane / 16;
 
-  constexpr int NOC = GATED ? 8 : 16 * NB;  // outputs per item
+  constexpr int NOC = (GATED ? 8 : 16) * NB;  // outputs per item
   const int xm = (p.x_rows + 15) / 16;
   const int num_n = p.n_out / NOC;
   const int x_items = xm * num_n;  // the extra expert's items come first
@@ -218,8 +221,10 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // 2080 us and the block 3614 -> 3406 us.  The plain launch on packed weights keeps the
   // issue order (C = 1: consecutive items on consecutive XCDs), each item one packed slot:
   // at T = 256 its w2 launch runs 1349 us against 1402 (C = 4), 1417 (C = 2) and 1407 us
-  // (C = 8), interleaved in one process.  The last, partial round keeps the issue order.
-  constexpr int C = GATED ? 32 : (PACKED ? 1 : 4);
+  // (C = 8), interleaved in one process.  The paired gated launch takes runs of 8 (T = 256:
+  // w13 1985 us against 2020 with 32 and 1997 with 16).  The last, partial round keeps the
+  // issue order.
+  constexpr int C = GATED ? (PAIR ? 8 : 32) : (PACKED ? 1 : 4);
   auto place = [&](int it) {
     if (ROUTE) return it;
     const int G = (int)gridDim.x;
@@ -270,9 +275,9 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
                            ((int64_t)e * num_n512 + P) * packed_tile_elems(nk32) +
                            packed_slot_off(nk32, ps);
       dw[0] = tb + (int64_t)(wvu * 4) * kPackStride;  // the slot's 32-k stages
-      if (PAIR)  // the second slot's stages
-        dw[1] = dw[0] + (packed_slot_off(nk32, ps + 1) - packed_slot_off(nk32, ps));
-      if (GATED) {
+      if (PAIR)  // the second slot's stages (gated: the `up` slot, four slots on)
+        dw[1] = dw[0] + (packed_slot_off(nk32, ps + (GATED ? 4 : 1)) - packed_slot_off(nk32, ps));
+      if (GATED && !PAIR) {
         const int hs = q5 & 1;
         wvo = (uint32_t)(lane < 32 ? (hs * 32 + lane) * 16
                                    : (packed_slot_off(nk32, ps + 4) - packed_slot_off(nk32, ps)) * 2 +
@@ -519,18 +524,25 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // load wrote it; MFMA row r16 is packed row p = r16 (gated: rows 0-7 the `gate` half,
   // 8-15 the `up` half, p = 8 hs + r16 % 8 of each slot), and its 8-k chunk g sits in the
   // lane slot 4 p + (g ^ (p / 4 % 4)).  The element offset of lane (r16, g) in a slab:
-  auto w_ofs = [&](int it) {
+  // Paired, block b reads slot b's slab (plain: slab 16 b + k; gated: rows 0-7 from the
+  // `gate` slab k, 8-15 from the `up` slab 16 + k, both of half hs = b), so the offset
+  // below includes the slab.
+  auto w_ofs = [&](int it, int b) {
     if constexpr (!PACKED) {
       return 0;
     } else if constexpr (GATED) {
-      const int hs = place(it) & 1;  // num_n is even
+      const int hs = PAIR ? b : place(it) & 1;  // num_n is even
       const int pp = r16 & 7;
+      if constexpr (PAIR) {
+        const int pr = 8 * hs + pp;  // row of the whole slot
+        return (r16 >> 3) * 16 * 512 + (4 * pr + (g ^ ((pr >> 2) & 3))) * 8;
+      }
       return (r16 >> 3) * 256 + (4 * pp + (g ^ (2 * hs + (pp >> 2)))) * 8;
     } else {
-      return (4 * r16 + (g ^ ((r16 >> 2) & 3))) * 8;
+      return b * 16 * 512 + (4 * r16 + (g ^ ((r16 >> 2) & 3))) * 8;
     }
   };
-  auto compute = [&](int buf, floatx4_t (&acc)[NB], int wofs) {
+  auto compute = [&](int buf, floatx4_t (&acc)[NB], const int (&wofs)[NB]) {
     const uint16_t* sb = ring + buf * SE;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
@@ -539,7 +551,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {  // block b: the item's slot b (paired) or its only one
         const uint4 wf =
-            PACKED ? *reinterpret_cast<const uint4*>(sb + (b * 16 + wv * 4 + q) * 512 + wofs)
+            PACKED ? *reinterpret_cast<const uint4*>(sb + (wv * 4 + q) * 512 + wofs[b])
                    : *reinterpret_cast<const uint4*>(sb + r16 * KS + ((c ^ r16) * 8));
         acc[b] = mfma16(wf, af, acc[b]);  // C[W row 4 g + i][token r16]
       }
@@ -606,7 +618,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
     for (int b = 0; b < NB; ++b) {
       float v;
       if (GATED) {
-        v = silu_mul(rsum(par, 0, j, c), rsum(par, 0, 8 + j, c));  // `gate` row j, `up` 8 + j
+        v = silu_mul(rsum(par, b, j, c), rsum(par, b, 8 + j, c));  // `gate` row j, `up` 8 + j
       } else {
         v = rsum(par, b, j, c);
         if (WEIGHTED && !extra) v = v * meta_w[slot][c];
@@ -667,7 +679,9 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
   int c_item = blockIdx.x, c_s = 0;
-  int wofs = w_ofs(c_item);
+  int wofs[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) wofs[b] = w_ofs(c_item, b);
   int pend = -1, par = 0;  // the item whose partial sums wait in red[par ^ 1], if any
 #pragma unroll 1
   for (int j = 0; j < total; ++j) {
@@ -697,7 +711,8 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       for (int b = 0; b < NB; ++b) acc[b] = floatx4_t{0.f, 0.f, 0.f, 0.f};
       c_s = 0;
       c_item += gridDim.x;
-      wofs = w_ofs(c_item);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) wofs[b] = w_ofs(c_item, b);
     }
   }
   if (pend >= 0) {
@@ -709,7 +724,7 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
 
 template <bool GATED, bool WEIGHTED, bool ROUTE, bool PACKED, bool PAIR = false>
 int launch_runs_t(const GemmArgs& a, int capacity, hipStream_t st) {
-  constexpr int NOC = GATED ? 8 : (PAIR ? 32 : 16);
+  constexpr int NOC = (GATED ? 8 : 16) * (PAIR ? 2 : 1);
   if (a.BM != 16 || (a.n_out % NOC) || (a.K % KS) || a.K / KS < (PAIR ? 2 : 1))
     return GLM52_EUNSUPPORTED;
   // packed: whole 512-row tiles (256 outputs gated), no atomic merge
@@ -737,8 +752,12 @@ int launch_runs(const GemmArgs& a, int capacity, bool gated, bool weighted, bool
       if (!gated || weighted) return GLM52_EUNSUPPORTED;
       return launch_runs_t<true, false, true, true>(a, capacity, st);
     }
+    // paired slots from two 512-k stages on (K >= 1024); gated from 1024 routed rows (at
+    // 512 the blocks hold about two real rows and the unpaired launch is 12 us faster)
+    if (gated && a.K >= 2 * KS && a.num_valid >= 1024)
+      return weighted ? launch_runs_t<true, true, false, true, true>(a, capacity, st)
+                      : launch_runs_t<true, false, false, true, true>(a, capacity, st);
     if (gated) return weighted ? launch_runs_t<true, true, false, true>(a, capacity, st) : launch_runs_t<true, false, false, true>(a, capacity, st);
-    // plain: paired slots from two 512-k stages on (K >= 1024)
     if (a.K >= 2 * KS)
       return weighted ? launch_runs_t<false, true, false, true, true>(a, capacity, st)
                       : launch_runs_t<false, false, false, true, true>(a, capacity, st);

@@ -640,11 +640,12 @@ def test_w512_item_dealing(gpu, bm):
     assert torch.equal(act4, act) and torch.equal(y4, y)
 
 
-@pytest.mark.parametrize("T", [1, 3, 16, 40])
+@pytest.mark.parametrize("T", [1, 3, 16, 40, 160])
 def test_packed_weight_stream_matches_in_place(gpu, T):
     """The decode weight stream (block size 16) on packed weights, routed and shared expert
     in one launch: the same bits as on the weights in place -- gated w13 + SwiGLU, weighted
-    w2 -- and the packed token-major tail within one bf16 rounding step of the in-place one
+    w2, both with two packed slots per item (K = 1024; the gated launch from 1024 routed
+    rows, T = 160) -- and the packed token-major tail within one bf16 rounding step of the in-place one
     (it adds in another order; 1e-3 absolute where the sum cancels) and both within bf16
     rounding of the fp32 reference."""
     E, H, I, k = 8, 1024, 1024, 8
