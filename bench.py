@@ -70,6 +70,10 @@ def parse():
     ap.add_argument("--pmc-step", default="w13", choices=("w13", "w2", "block"),
                     help="(with --pmc-child) the launch profiled: the block's w13 launch, its "
                          "w2 launch, or the whole block")
+    ap.add_argument("--item-trace", action="store_true",
+                    help="only record, per workgroup, when each prefill tile launch (w13, w2) of "
+                         "the block at the first --tokens value starts and ends, its items and "
+                         "XCD (glm52_debug_item_trace), print the per-XCD finish spread and exit")
     ap.add_argument("--copy-probe", action="store_true",
                     help="first run a plain 256 MiB device copy three times: the known-size "
                          "dispatch that scales rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
@@ -114,6 +118,10 @@ def main() -> int:
     torch.cuda.synchronize()
     log(f"weights ready in {time.time() - t0:.1f}s ({PW.nbytes() / 1e9:.1f} GB packed)")
     flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)  # 1 GiB
+    if args.item_trace:
+        T = int(args.tokens.split(",")[0])
+        print(json.dumps({"item_trace": item_trace(T, PW, flush_buf, dev)}), flush=True)
+        return 0
     if args.pmc_child:
         T = int(args.tokens.split(",")[0])
         fe = front_end(T, bias="zipf" if T == 8192 else "normal")
@@ -537,6 +545,62 @@ def prenorm_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
             "gain": round(u_us / min(h_us, f_us), 3),
             "roofline_us": round(roof, 2), "roofline_frac": round(roof / min(h_us, f_us), 4),
             "bound": kc.bound()}
+
+
+def item_trace(T: int, PW, flush_buf, dev) -> dict:
+    """The block at T (Zipf routing at 8192): after 50 ms of blocks, its w13 and its w2
+    launch once each (after the flush) with the per-workgroup record on; per launch, each
+    workgroup's finish time from the launch's first start, summarised per XCD."""
+    import torch
+
+    from fusion_amd import _lib
+    from fusion_amd.block import MoEBlock
+    from fusion_amd.problem import front_end
+
+    fe = front_end(T, bias="zipf" if T == 8192 else "normal")
+    x, r = fe.x.to(dev), fe.r.to(dev)
+    blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), PW)
+    t_end = time.perf_counter() + SETTLE_MS * 1e-3
+    while time.perf_counter() < t_end:
+        flush_buf.zero_()
+        blk(x, r)
+        torch.cuda.synchronize()
+    rec = torch.zeros(256 * 4, dtype=torch.int64, device=dev)
+    out = {"T": T, "block_m": blk.bm, "clock": "s_memrealtime, 100 MHz"}
+    for name, step in (("w13", blk.w13_step), ("w2", blk.w2_step)):
+        rec.zero_()
+        flush_buf.zero_()
+        torch.cuda.synchronize()
+        _lib.call("glm52_debug_item_trace", _lib.ptr(rec), rec.numel() * 8)
+        try:
+            step()
+            torch.cuda.synchronize()
+        finally:
+            _lib.call("glm52_debug_item_trace", None, 0)
+        v = rec.view(256, 4).cpu().tolist()
+        rows = [w for w in v if w[0] > 0]
+        t0 = min(w[0] for w in rows)
+        ends = [(w[1] - t0) / 100.0 for w in rows]
+        xcd = {}
+        for w, e in zip(rows, ends):
+            xcd.setdefault(int(w[3]), []).append((e, int(w[2])))
+        per = {str(k): {"workgroups": len(l), "end_min_us": round(min(e for e, _ in l), 1),
+                        "end_max_us": round(max(e for e, _ in l), 1),
+                        "spread_us": round(max(e for e, _ in l) - min(e for e, _ in l), 1),
+                        "items": sum(n for _, n in l)}
+               for k, l in sorted(xcd.items())}
+        items = [int(w[2]) for w in rows]
+        out[name] = {"workgroups": len(rows), "span_us": round(max(ends), 1),
+                     "end_min_us": round(min(ends), 1),
+                     "spread_us": round(max(ends) - min(ends), 1),
+                     "xcd_end_max_spread_us": round(max(p["end_max_us"] for p in per.values())
+                                                    - min(p["end_max_us"] for p in per.values()), 1),
+                     "max_spread_in_xcd_us": max(p["spread_us"] for p in per.values()),
+                     "items_per_wg_min": min(items), "items_per_wg_max": max(items),
+                     "items": sum(items), "per_xcd": per}
+        log(f"item trace {name}: span {out[name]['span_us']} us, finish spread "
+            f"{out[name]['spread_us']} us")
+    return out
 
 
 def calibrate(dev) -> list:

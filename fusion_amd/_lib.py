@@ -74,6 +74,7 @@ SIGNATURES: dict[str, list] = {
     "glm52_block_merge": [_P, _L, _L, _P, _L, _P, _L, _P, _L, _I, _I, _P],
     "glm52_selftest_mfma_layout": [_P, _P],
     "glm52_stream_read": [_P, _L, _I, _I, _P, _P],
+    "glm52_debug_item_trace": [_P, _L],
 }
 
 # name -> (argument types, return type) for entry points that do not return a status

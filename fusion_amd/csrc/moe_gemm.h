@@ -172,6 +172,9 @@ struct GemmArgs {
   // 512-row tile mapping: the set of per-XCD item counters this launch deals its items
   // from (set by the launcher)
   int deal_set;
+  // 512-row tile mapping: null, or a record of 4 words per workgroup (start and end on the
+  // 100 MHz wall clock, items run, XCD) written at the workgroup's end (glm52_debug_item_trace)
+  unsigned long long* wg_trace;
 };
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));

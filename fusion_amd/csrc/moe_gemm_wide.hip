@@ -365,8 +365,13 @@ constexpr int kDealSets = 64;
 constexpr int kDealStride = 256;  // ints per set: XCD x's counter at 16 x, the exits at 128
 __device__ __align__(256) int g_w512_deal[kDealSets * kDealStride];
 
+// The host side of glm52_debug_item_trace: the record the next launches write, or null.
+std::atomic<unsigned long long*> g_item_trace{nullptr};
+
 template <int MT, int NTW, bool GATED, bool WEIGHTED, bool PACKED, int EPI = 0>
 __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
+  const unsigned long long t_start = p.wg_trace ? __builtin_amdgcn_s_memrealtime() : 0ull;
+  int n_run = 0;  // items this workgroup ran (the trace record)
   constexpr int BKS = 32;          // k per stage
   constexpr int WN = NTW / 128;    // waves along W
   constexpr int WM = 4 / WN;       // waves along the tokens
@@ -473,6 +478,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       e = 0;
       w_once = nbx == 1;
     }
+    ++n_run;
     const int n0 = pid_n * NO;
     const int P = pid_n / SPLIT, sub = pid_n % SPLIT;  // the packed 512-row tile and half
     // the item's operands: the routed rows through the layout, the extra expert's directly
@@ -716,6 +722,13 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     k = __builtin_amdgcn_readfirstlane(wg_xcd + *slot);
     __syncthreads();  // every wave has the index before the next prologue refills the ring
   }
+  if (p.wg_trace && tid == 0) {  // start, end, items, XCD (hardware register XCC_ID)
+    unsigned long long* rec = p.wg_trace + (int64_t)blockIdx.x * 4;
+    rec[0] = t_start;
+    rec[1] = __builtin_amdgcn_s_memrealtime();
+    rec[2] = (unsigned long long)n_run;
+    rec[3] = (unsigned long long)(__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15);
+  }
   // the last workgroup out clears the set for the next launch that uses it
   if (tid == 0 && __hip_atomic_fetch_add(deal + 128, 1, __ATOMIC_RELAXED,
                                          __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1) {
@@ -731,6 +744,7 @@ int launch_w512(const GemmArgs& a_in, int capacity, hipStream_t st) {
   static std::atomic<unsigned> next_set{0};
   GemmArgs a = a_in;
   a.deal_set = (int)(next_set.fetch_add(1, std::memory_order_relaxed) % kDealSets);
+  a.wg_trace = g_item_trace.load(std::memory_order_relaxed);
   if ((a.n_out % (GATED ? 256 : 512)) || (a.K % 64)) return GLM52_EUNSUPPORTED;
   const int x_blocks = (a.Wp && a.Wx && a.x_rows > 0) ? (a.x_rows + MT - 1) / MT : 0;
   const int items_max = (capacity / MT + x_blocks) * (a.n_out / NO);
@@ -830,6 +844,15 @@ int launch_wide512(const GemmArgs& a, int capacity, bool gated, bool weighted, h
   return weighted ? launch_w512_bm<false, true>(a, capacity, st) : launch_w512_bm<false, false>(a, capacity, st);
 }
 
+}  // namespace glm52
+
+extern "C" int glm52_debug_item_trace(void* buf, int64_t bytes) {
+  if (buf && bytes < 256 * 4 * (int64_t)sizeof(unsigned long long)) return GLM52_EINVAL;
+  g_item_trace.store(static_cast<unsigned long long*>(buf), std::memory_order_relaxed);
+  return GLM52_OK;
+}
+
+namespace glm52 {
 int64_t pack_wide512(const uint16_t* w, int64_t swe, int64_t swn, int E, int n_out, int k,
                      int gate_up_offset, bool gated, uint16_t* out, hipStream_t st,
                      int64_t swk) {

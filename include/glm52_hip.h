@@ -401,6 +401,14 @@ int glm52_stream_read(const void* buf, int64_t bytes, int nontemporal, int grid,
  * No counterpart in the reference. */
 int glm52_selftest_mfma_layout(float* out, hipStream_t stream);
 
+/* Measurement hook of the prefill tile (the 512-row and 256 x 256 tile launches of
+ * glm52_moe_gemm, glm52_moe_gemm_packed(_shared), glm52_oproj_gemm): with `buf` set (at least
+ * 256 x 4 words of device memory), every later launch writes, per workgroup w, words
+ * 4w .. 4w+3 = its start and end on the 100 MHz wall clock, the items it ran and its XCD;
+ * with `buf` null (the default) nothing is recorded.  Process-wide; not for overlapping
+ * launches.  No counterpart in the reference: it shows how the items are dealt. */
+int glm52_debug_item_trace(void* buf, int64_t bytes);
+
 #ifdef __cplusplus
 }
 #endif

@@ -640,6 +640,35 @@ def test_w512_item_dealing(gpu, bm):
     assert torch.equal(act4, act) and torch.equal(y4, y)
 
 
+def test_w512_item_trace_record(gpu):
+    """The prefill tile's measurement hook: every workgroup's record has its start before
+    its end, an XCD below 8, and the records' item counts add up to the launch's items (one
+    item per 256-token block and 256-output tile, T = 1000 on 8 experts); with the hook off
+    again nothing more is written."""
+    T, E, H, I, k = 1000, 8, 512, 256, 8
+    a, w13, w2, ids, tw = _gemm_problem(T, E, H, I, k, 811, gpu)
+    w2p = KG.pack_w512(w2.to(gpu), H, 0, False)
+    act = (torch.randn(T * k, I, generator=torch.Generator().manual_seed(3)) * 0.5).to(BF16).to(gpu)
+    sti, eids, ntp = moe_align_block_size(ids.to(gpu), 256, E)
+    y = torch.empty(T * k, H, dtype=BF16, device=gpu)
+    rec = torch.zeros(256 * 4, dtype=torch.int64, device=gpu)
+    _lib.call("glm52_debug_item_trace", _lib.ptr(rec), rec.numel() * 8)
+    try:
+        KG.moe_gemm_packed(act, 1, w2p, y, None, sti, eids, ntp, T * k, H, False, {"BLOCK_M": 256})
+        torch.cuda.synchronize()
+    finally:
+        _lib.call("glm52_debug_item_trace", None, 0)
+    r = rec.view(256, 4).cpu()
+    used = r[:, 0] > 0
+    assert bool((r[used, 1] >= r[used, 0]).all()) and bool((r[used, 3] < 8).all())
+    blocks = int(ntp.item()) // 256
+    assert int(r[used, 2].sum()) == blocks * (H // 256)
+    rec.zero_()
+    KG.moe_gemm_packed(act, 1, w2p, y, None, sti, eids, ntp, T * k, H, False, {"BLOCK_M": 256})
+    torch.cuda.synchronize()
+    assert int(rec.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("T", [1, 3, 16, 40, 160])
 def test_packed_weight_stream_matches_in_place(gpu, T):
     """The decode weight stream (block size 16) on packed weights, routed and shared expert

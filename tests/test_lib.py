@@ -132,3 +132,10 @@ def test_router_select_workspace_query():
     assert q(8192) == 4 * (256 + 8192) * 4 + 256 + 4 * 8192 * 256 * 4
     # 2048 tokens: 32 blocks of 64 tokens x 8 K slices
     assert q(2048) == 8 * (256 + 2048) * 4 + 256 + 8 * 2048 * 256 * 4
+
+
+def test_item_trace_hook_checks_its_buffer():
+    # the record needs 256 workgroups x 4 words; null turns it off (no GPU call either way)
+    with pytest.raises(RuntimeError, match="invalid argument"):
+        _lib.call("glm52_debug_item_trace", 4096, 8)
+    _lib.call("glm52_debug_item_trace", None, 0)
