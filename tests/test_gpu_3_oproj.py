@@ -41,7 +41,7 @@ def _run(chain):
 
 
 @pytest.mark.parametrize("M,K", [(1, 32768), (4, 32768), (16, 32768), (32, 32768),
-                                 (256, 16384), (2048, 16384)])
+                                 (256, 16384), (300, 16384), (2048, 16384), (2600, 16384)])
 def test_oproj_chains(gpu, M, K):
     say(f"oproj M={M} K={K}")
     a, w_nk, b, r = _problem(M, K, gpu)
