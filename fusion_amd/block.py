@@ -18,7 +18,7 @@ the routing computed live instead of frozen, and the tail fused):
                                 (5+6 and 7+8 are one launch each: moe_gemm_shared when
                                  streaming weights, moe_gemm_packed_shared at prefill)
     9. merge + ResAdd           out = bf16(sum_k Y[t, k] + h + s)         block_merge
-                                (T <= 4: 7-9 are one launch, down_token_major:
+                                (T = 1: 7-9 are one launch, down_token_major:
                                  out = bf16(sum_k w * (act . w2^T) + shared + h), fp32
                                  over all experts, one rounding -- the reference's
                                  token-major strategy #9(b))
@@ -198,10 +198,12 @@ class MoEBlock:
         # weight-streaming decode runs the shared expert inside the routed launches
         self.shared_fused = self.bm == 16
         self.front_fused = T <= DECODE_FRONT_MAX_T and self.shared_fused
-        # decode tail: the token-major down GEMV sums each token's experts, the shared
-        # expert and h in one launch (no Y rows, no merge launch)
-        self.token_major = (self.front_fused and variant is None) if token_major is None \
-            else bool(token_major)
+        # decode tail at T = 1: the token-major down GEMV sums the token's experts, the
+        # shared expert and h in one launch (no Y rows, no merge launch); from T = 2 the
+        # weight stream with paired slots + the merge is faster (whole blocks: T = 2 221.2
+        # against 228.7 us, T = 3 305.7 against 321.6 us; T = 1 128.2 against 125.3 us)
+        self.token_major = (self.front_fused and variant is None and T == 1) \
+            if token_major is None else bool(token_major)
         if self.token_major and not self.shared_fused:
             # the token-major tail reads the shared expert's activations, which only the
             # weight-streaming w13 launch (block size 16) writes before the tail
