@@ -317,7 +317,14 @@ int launch_wide(const GemmArgs& a, int capacity, bool gated, bool weighted, hipS
 // ((p >> 2) & 1) * 16 + (p >> 3) * 4 + (p & 3); a lane's 16 results of a 32 x 32 block are
 // then 16 consecutive outputs of one token, written with two 16-byte stores.  A gated tile
 // pairs `gate` row n and `up` row n in the same lane and register, so SwiGLU runs in
-// registers.
+// registers.  The tokens and routing weights of an item's rows are loaded once, before
+// its first store, and kept in the ring buffer the last stage has freed.
+//
+// Registers.  The kernel holds 256 accumulators and the fragments of two stages: near the
+// 512-register limit, a value the compiler hoists out of the item loop to keep live across
+// it (the lane's load offsets, the ring's addresses) is spilled, and its reload waits for
+// every load in flight.  Such values are formed per item from opaque copies of the lane
+// index and the ring's address.
 // ------------------------------------------------------------------------------------
 namespace {
 
@@ -419,9 +426,6 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
   // fragment reads: lane (l32, h) reads logical chunk 2 ks + h of row base + l32 (base % 32 == 0)
   const int rd0 = l32 * BKS + (((0 + h) ^ ((l32 >> 2) & 3)) * 8);
   const int rd1 = l32 * BKS + (((2 + h) ^ ((l32 >> 2) & 3)) * 8);
-  // load slots: lane -> row lane / 4 of the instruction's 16-row slab, physical chunk lane % 4
-  const int dr = lane >> 2;
-  const int dc = (lane & 3) ^ ((dr >> 2) & 3);  // the logical chunk that lands in that slot
   const uint32_t ring_base = lds_addr(ring);
   // the next item's index passes from wave 0 to the others through the first word of the
   // ring buffer of the last stage: no load issued past the last stage lands there, and
@@ -490,11 +494,23 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       return xs ? (row0 + r < p.x_rows ? row0 + r : p.x_rows) : p.sti[row0 + r];
     };
 
+    // The lane index through an opaque copy: the lane's offsets below are computed here, per
+    // item, rather than hoisted out of the item loop to stay live (and be spilled) across it.
+    int il = lane;
+    asm volatile("" : "+v"(il));
+    // load slots: lane -> row il / 4 of the instruction's 16-row slab, physical chunk il % 4
+    const int dr = il >> 2;
+    const int dc = (il & 3) ^ ((dr >> 2) & 3);  // the logical chunk that lands in that slot
+    // the ring's address likewise: the prologue's LDS addresses (m0) are then formed per
+    // item, not precomputed once and held across the item loop
+    uint32_t rb = ring_base;
+    asm volatile("" : "+s"(rb));
+
     // real tokens fill a prefix of the block: every wave counts them (no LDS, no barrier)
     int nv_rows = 0;
 #pragma unroll
     for (int q = 0; q < MT; q += kWave)
-      nv_rows += __popcll(__ballot(q + lane < MT && tok_of(q + lane) < nvalid));
+      nv_rows += __popcll(__ballot(q + il < MT && tok_of(q + il) < nvalid));
     nv_rows = __builtin_amdgcn_readfirstlane(nv_rows);
     const int nvf = __builtin_amdgcn_readfirstlane(max(0, min(TF, (nv_rows - wm * TPW + 31) / 32)));
 
@@ -510,10 +526,10 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
       if (PACKED) {
         // load slot sub * 32 / SPLIT + wv * WI + i of the 512-row tile: nk KB per slot
         wvoff[i] = (uint32_t)(packed_slot_off(nk, sub * (32 / SPLIT) + wv * WI + i) * 2 +
-                              lane * 16);
+                              il * 16);
       } else {
         const int slab = sub * (NTW / RPI) + wv * WI + i;  // 1 KB slab of the 512-row tile
-        const int row = P * NO512 + w512_row(GATED, p.gu_off, slab / 8, slab % 8, lane);
+        const int row = P * NO512 + w512_row(GATED, p.gu_off, slab / 8, slab % 8, il);
         wvoff[i] = (uint32_t)(((int64_t)row * p.swn + dc * 8) * 2);
       }
     }
@@ -531,7 +547,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     auto issue_one = [&](int i, int kt) {  // load instruction i of stage kt (clamped)
       const bool past = kt >= nk;  // wave-uniform
       const int kc = min(kt, nk - 1) * BKS;
-      const uint32_t sb = ring_base + (uint32_t)((kt % NSTAGE) * SELEM * 2);
+      const uint32_t sb = rb + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
         const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * kPackStride : wexp + kc;
         const uint32_t vo = past ? 0u : wvoff[i];
@@ -633,66 +649,106 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
         stage(kt + 1, std::integral_constant<int, 1>{});
       }
 
+      if constexpr (EPI == 0) {
+        // The lane index through an opaque copy, as in the item's set-up; the tokens and
+        // routing weights of the wave's rows are loaded together, before any store, into the
+        // ring buffer of stage nk - 1 (free here: every wave has read its fragments, no load
+        // past the last stage lands in it) and read back per 32-row block.  vmcnt also
+        // counts stores, so a token loaded after a block's stores would wait for them.
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int el32 = ln % 32, eh = ln / 32;
+        int* const etok =
+            reinterpret_cast<int*>(ring + ((nk - 1) % NSTAGE) * SELEM) + wvu * 2 * TPW;
+        float* const ewgt = reinterpret_cast<float*>(etok + TPW);
+        static_assert(TPW % 64 == 0 && 4 * 2 * TPW * 4 <= SELEM * 2, "epilogue rows");
+        {
+          int qt[TPW / 64];
 #pragma unroll
-      for (int t = 0; t < NV; ++t) {
-        const int tok = tok_of(wm * TPW + t * 32 + l32);
-        if (tok >= nvalid) continue;
-        uint16_t* crow = EPI >= 2 ? nullptr
-                                  : (xs ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm);
-        if (GATED) {
+          for (int j = 0; j < TPW / 64; ++j) qt[j] = tok_of(wm * TPW + j * 64 + ln);
 #pragma unroll
-          for (int fp = 0; fp < 2; ++fp) {
-            float v[16];
-#pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = silu_mul(acc[fp][t][i], acc[fp + 2][t][i]);
-            uint16_t* dst = crow + n0 + wn * 64 + fp * 32 + h * 16;
-            *reinterpret_cast<uint4*>(dst) = pack8(v);
-            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+          for (int j = 0; j < TPW / 64; ++j) {
+            etok[j * 64 + ln] = qt[j];
+            if (WEIGHTED) ewgt[j * 64 + ln] = (!xs && qt[j] < nvalid) ? p.topw[qt[j]] : 1.f;
           }
-        } else {
-          float wgt = 1.f;
-          if (WEIGHTED && !xs) wgt = p.topw[tok];
+        }
 #pragma unroll
-          for (int f = 0; f < 4; ++f) {
-            float v[16];
+        for (int t = 0; t < NV; ++t) {
+          const int tok = etok[t * 32 + el32];
+          if (tok >= nvalid) continue;
+          uint16_t* const crow = xs ? p.Cx + (int64_t)tok * p.scx : p.C + (int64_t)tok * p.scm;
+          if (GATED) {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
-            const int col = n0 + wn * 128 + f * 32 + h * 16;
-            if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
-              const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
-              float rf[16];
-              unpack8(*reinterpret_cast<const uint4*>(rr), rf);
-              unpack8(*reinterpret_cast<const uint4*>(rr + 8), rf + 8);
+            for (int fp = 0; fp < 2; ++fp) {
+              float v[16];
 #pragma unroll
-              for (int i = 0; i < 16; ++i) v[i] = v[i] + rf[i];
+              for (int i = 0; i < 16; ++i) v[i] = silu_mul(acc[fp][t][i], acc[fp + 2][t][i]);
+              uint16_t* dst = crow + n0 + wn * 64 + fp * 32 + eh * 16;
+              *reinterpret_cast<uint4*>(dst) = pack8(v);
+              *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
             }
-            if (EPI == 2) {  // accumulate into the fp32 output
-              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+          } else {
+            const float wgt = WEIGHTED ? ewgt[t * 32 + el32] : 1.f;
 #pragma unroll
-              for (int q = 0; q < 4; ++q) {
-                float4 o = dst[q];
-                o.x += v[4 * q];
-                o.y += v[4 * q + 1];
-                o.z += v[4 * q + 2];
-                o.w += v[4 * q + 3];
-                dst[q] = o;
-              }
-            } else if (EPI == 3) {  // fp32 partial sums, stored
-              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+            for (int f = 0; f < 4; ++f) {
+              float v[16];
 #pragma unroll
-              for (int q = 0; q < 4; ++q)
-                dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-            } else if (EPI == 4) {  // atomic merge into row tok / top_k, two outputs a word
-              uint16_t* dst = p.C + (int64_t)(tok / p.merge_topk) * p.scm + col;
-#pragma unroll
-              for (int q = 0; q < 8; ++q) atomic_add_bf16x2(dst + 2 * q, v[2 * q], v[2 * q + 1]);
-            } else {
-              uint16_t* dst = crow + col;
+              for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
+              uint16_t* dst = crow + n0 + wn * 128 + f * 32 + eh * 16;
               *reinterpret_cast<uint4*>(dst) = pack8(v);
               *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
             }
           }
         }
+      } else {
+#pragma unroll
+      for (int t = 0; t < NV; ++t) {  // o_proj epilogues and the atomic merge (plain only)
+        const int tok = tok_of(wm * TPW + t * 32 + l32);
+        if (tok >= nvalid) continue;
+        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;
+        float wgt = 1.f;
+        if (WEIGHTED && !xs) wgt = p.topw[tok];
+#pragma unroll
+        for (int f = 0; f < 4; ++f) {
+          float v[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
+          const int col = n0 + wn * 128 + f * 32 + h * 16;
+          if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
+            const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
+            float rf[16];
+            unpack8(*reinterpret_cast<const uint4*>(rr), rf);
+            unpack8(*reinterpret_cast<const uint4*>(rr + 8), rf + 8);
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = v[i] + rf[i];
+          }
+          if (EPI == 2) {  // accumulate into the fp32 output
+            float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float4 o = dst[q];
+              o.x += v[4 * q];
+              o.y += v[4 * q + 1];
+              o.z += v[4 * q + 2];
+              o.w += v[4 * q + 3];
+              dst[q] = o;
+            }
+          } else if (EPI == 3) {  // fp32 partial sums, stored
+            float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+          } else if (EPI == 4) {  // atomic merge into row tok / top_k, two outputs a word
+            uint16_t* dst = p.C + (int64_t)(tok / p.merge_topk) * p.scm + col;
+#pragma unroll
+            for (int q = 0; q < 8; ++q) atomic_add_bf16x2(dst + 2 * q, v[2 * q], v[2 * q + 1]);
+          } else {  // EPI 1: bf16(acc + R)
+            uint16_t* dst = crow + col;
+            *reinterpret_cast<uint4*>(dst) = pack8(v);
+            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+          }
+        }
+      }
       }
       }
     };
