@@ -474,7 +474,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
         k = fetch_now();
         continue;
       }
-      e = p.eids[pid_m];
+      e = eb;  // the blocks mb .. me - 1 all hold expert eb
     } else {
       const int Lx = xcd * per_xcd_x + (k - n_r);
       pid_n = Lx / nbx;
@@ -506,6 +506,12 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     uint32_t rb = ring_base;
     asm volatile("" : "+s"(rb));
 
+    // the tokens of the lane's staged rows, loaded beside the real-row count below (a row
+    // past the real ones then re-reads the block's first row)
+    int trl[AI];
+#pragma unroll
+    for (int i = 0; i < AI; ++i) trl[i] = tok_of(wv * (MT / 4) + i * RPI + dr);
+    const int tr0 = tok_of(0);
     // real tokens fill a prefix of the block: every wave counts them (no LDS, no barrier)
     int nv_rows = 0;
 #pragma unroll
@@ -537,7 +543,7 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < AI; ++i) {
       const int rl = wv * (MT / 4) + i * RPI + dr;
-      avoff[i] = (uint32_t)((tok_of(rl < nv_rows ? rl : 0) / a_div) * (int)sam + dc * 8) * 2u;
+      avoff[i] = (uint32_t)(((rl < nv_rows ? trl[i] : tr0) / a_div) * (int)sam + dc * 8) * 2u;
     }
 
     // the previous item's output stores and loads are done before this item's are counted
