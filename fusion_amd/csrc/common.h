@@ -71,11 +71,10 @@ GLM52_DEV double wave_sum_f64(double v) {
   return v;
 }
 
-// silu(g) * u in fp32, the SwiGLU of `glm52/reference.py:36-40`.
-// silu(g) * u with the hardware reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE divide,
-// whose ten-instruction expansion dominated the prefill GEMM's gated epilogue; the result is
-// rounded to bf16 by every caller.  g -> -inf: exp overflows, the reciprocal is 0, as the
-// quotient was.
+// silu(g) * u in fp32, the SwiGLU of `glm52/reference.py:36-40`, with the hardware
+// reciprocal (v_rcp_f32, 1 ulp) in place of an IEEE divide, whose ten-instruction expansion
+// dominated the prefill GEMM's gated epilogue; every caller rounds the result to bf16.
+// g -> -inf: exp overflows and the reciprocal is 0, as the quotient was.
 GLM52_DEV float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }

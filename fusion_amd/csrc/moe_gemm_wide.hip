@@ -708,53 +708,53 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
         }
       } else {
 #pragma unroll
-      for (int t = 0; t < NV; ++t) {  // o_proj epilogues and the atomic merge (plain only)
-        const int tok = tok_of(wm * TPW + t * 32 + l32);
-        if (tok >= nvalid) continue;
-        uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;
-        float wgt = 1.f;
-        if (WEIGHTED && !xs) wgt = p.topw[tok];
+        for (int t = 0; t < NV; ++t) {  // o_proj epilogues and the atomic merge (plain only)
+          const int tok = tok_of(wm * TPW + t * 32 + l32);
+          if (tok >= nvalid) continue;
+          uint16_t* crow = EPI >= 2 ? nullptr : p.C + (int64_t)tok * p.scm;
+          float wgt = 1.f;
+          if (WEIGHTED && !xs) wgt = p.topw[tok];
 #pragma unroll
-        for (int f = 0; f < 4; ++f) {
-          float v[16];
+          for (int f = 0; f < 4; ++f) {
+            float v[16];
 #pragma unroll
-          for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
-          const int col = n0 + wn * 128 + f * 32 + h * 16;
-          if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
-            const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
-            float rf[16];
-            unpack8(*reinterpret_cast<const uint4*>(rr), rf);
-            unpack8(*reinterpret_cast<const uint4*>(rr + 8), rf + 8);
+            for (int i = 0; i < 16; ++i) v[i] = WEIGHTED ? acc[f][t][i] * wgt : acc[f][t][i];
+            const int col = n0 + wn * 128 + f * 32 + h * 16;
+            if (EPI == 1 || (EPI == 2 && p.R)) {  // + the residual row, in fp32 (epilogue 3: none)
+              const uint16_t* rr = p.R + (int64_t)tok * p.srm + col;
+              float rf[16];
+              unpack8(*reinterpret_cast<const uint4*>(rr), rf);
+              unpack8(*reinterpret_cast<const uint4*>(rr + 8), rf + 8);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = v[i] + rf[i];
-          }
-          if (EPI == 2) {  // accumulate into the fp32 output
-            float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float4 o = dst[q];
-              o.x += v[4 * q];
-              o.y += v[4 * q + 1];
-              o.z += v[4 * q + 2];
-              o.w += v[4 * q + 3];
-              dst[q] = o;
+              for (int i = 0; i < 16; ++i) v[i] = v[i] + rf[i];
             }
-          } else if (EPI == 3) {  // fp32 partial sums, stored
-            float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
+            if (EPI == 2) {  // accumulate into the fp32 output
+              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
-          } else if (EPI == 4) {  // atomic merge into row tok / top_k, two outputs a word
-            uint16_t* dst = p.C + (int64_t)(tok / p.merge_topk) * p.scm + col;
+              for (int q = 0; q < 4; ++q) {
+                float4 o = dst[q];
+                o.x += v[4 * q];
+                o.y += v[4 * q + 1];
+                o.z += v[4 * q + 2];
+                o.w += v[4 * q + 3];
+                dst[q] = o;
+              }
+            } else if (EPI == 3) {  // fp32 partial sums, stored
+              float4* dst = reinterpret_cast<float4*>(p.C32 + (int64_t)tok * p.scm + col);
 #pragma unroll
-            for (int q = 0; q < 8; ++q) atomic_add_bf16x2(dst + 2 * q, v[2 * q], v[2 * q + 1]);
-          } else {  // EPI 1: bf16(acc + R)
-            uint16_t* dst = crow + col;
-            *reinterpret_cast<uint4*>(dst) = pack8(v);
-            *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+              for (int q = 0; q < 4; ++q)
+                dst[q] = make_float4(v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]);
+            } else if (EPI == 4) {  // atomic merge into row tok / top_k, two outputs a word
+              uint16_t* dst = p.C + (int64_t)(tok / p.merge_topk) * p.scm + col;
+#pragma unroll
+              for (int q = 0; q < 8; ++q) atomic_add_bf16x2(dst + 2 * q, v[2 * q], v[2 * q + 1]);
+            } else {  // EPI 1: bf16(acc + R)
+              uint16_t* dst = crow + col;
+              *reinterpret_cast<uint4*>(dst) = pack8(v);
+              *reinterpret_cast<uint4*>(dst + 8) = pack8(v + 8);
+            }
           }
         }
-      }
       }
       }
     };
