@@ -222,8 +222,9 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   // issue order (C = 1: consecutive items on consecutive XCDs), each item one packed slot:
   // at T = 256 its w2 launch runs 1349 us against 1402 (C = 4), 1417 (C = 2) and 1407 us
   // (C = 8), interleaved in one process.  The paired gated launch takes runs of 8 (T = 256:
-  // w13 1985 us against 2020 with 32 and 1997 with 16).  The last, partial round keeps the
-  // issue order.
+  // w13 1985 us against 2020 with 32 and 1997 with 16); the paired plain launch keeps C = 1
+  // (w2 1170 us against 1329, 1175 and 1184 with 2, 4 and 8).  The last, partial round
+  // keeps the issue order.
   constexpr int C = GATED ? (PAIR ? 8 : 32) : (PACKED ? 1 : 4);
   auto place = [&](int it) {
     if (ROUTE) return it;
