@@ -67,9 +67,11 @@ def parse():
     ap.add_argument("--pmc-child", action="store_true",
                     help="(internal) the process profiled for roofline.traffic: three 256 MiB "
                          "copies, then the block's w13 launch at the first --tokens value")
-    ap.add_argument("--pmc-step", default="w13", choices=("w13", "w2", "block"),
+    ap.add_argument("--pmc-step", default="w13",
+                    choices=("w13", "w2", "block", "tail", "tail-rowmajor"),
                     help="(with --pmc-child) the launch profiled: the block's w13 launch, its "
-                         "w2 launch, or the whole block")
+                         "w2 launch, the whole block, its token-major tail (T = 1, packed "
+                         "weights), or the same tail on the row-major weights")
     ap.add_argument("--item-trace", action="store_true",
                     help="only record, per workgroup, when each prefill tile launch (w13, w2) of "
                          "the block at the first --tokens value starts and ends, its items and "
@@ -129,7 +131,18 @@ def main() -> int:
         blk = MoEBlock(T, fe.w_norm.to(dev), fe.wgt.to(dev), fe.bias.to(dev), PW)
         blk(x, r)
         torch.cuda.synchronize()
-        step = {"w13": blk.w13_step, "w2": blk.w2_step, "block": lambda: blk(x, r)}[args.pmc_step]
+        from fusion_amd.kernels import moe_down_merge as KD
+
+        out_rm = torch.empty_like(blk.out)
+
+        def tail_rowmajor():  # the same sum on the row-major weights (the layout comparison)
+            KD.launch_down_token_major(blk.act, W.w2, out_rm, blk.topw, blk.topi, blk.h,
+                                       blk.topk, {}, True, blk.act_s, W.w2s)
+
+        step = {"w13": blk.w13_step, "w2": blk.w2_step, "block": lambda: blk(x, r),
+                "tail": blk.tail, "tail-rowmajor": tail_rowmajor}[args.pmc_step]
+        if args.pmc_step.startswith("tail") and not blk.token_major:
+            raise SystemExit("--pmc-step tail needs the token-major tail (--tokens 1)")
         for _ in range(PMC_LAUNCHES):
             flush_buf.zero_()
             step()
