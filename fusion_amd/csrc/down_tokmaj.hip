@@ -119,12 +119,17 @@ __global__ __launch_bounds__(256) void down_tokmaj_kernel(
 // + (q % 2) * 8 + phi32(p), p = 0 .. 15; the slot holds their K / 32 stages of 1 KB each,
 // kPackStride apart (packed_slot_off), lane l's 16 bytes holding row p = l / 4, 8-k chunk
 // (l % 4) ^ (p / 4 % 4).  Workgroup (s, t) owns slot s (tile s / 32, slot s % 32) of token
-// t: wave w takes the pieces of QS stages that start at stages QS w and QS (4 + w), so the
-// four waves read 4 QS stages of the slot at a time; every load reads one stage's whole 1 KB,
-// and a lane keeps one fp32 partial of its row over all pieces.  The 4 lanes of a row, then the 4 waves, meet in a fixed order.  The pieces flow
-// through two register buffers, so a wave has two pieces' loads in flight; four waves per
-// workgroup let two workgroups share a CU (about 210 VGPRs), so at T = 1 and N = 6144 the
-// 384 workgroups run in a single round.
+// t: wave w takes the pieces of QS stages that start at stages QS b and QS (b + 4) with
+// b = (w + g) % 8 for the workgroup's group of 8 slots g = s / 8, so the four waves read
+// 4 QS stages of the slot at a time; every load reads one stage's whole 1 KB, and a lane
+// keeps one fp32 partial of its row over all pieces.  The 4 lanes of a row, then the 4
+// waves, meet in a fixed order.  The pieces flow through two register buffers, so a wave
+// has two pieces' loads in flight; four waves per workgroup let two workgroups share a CU
+// (about 210 VGPRs), so at T = 1 and N = 6144 the 384 workgroups run in a single round.
+// The rotation by g: the workgroups advance in step, and without it every group would
+// read the same stages of the same expert at once, at addresses a power of two apart (the
+// group stride, NK * 8 KB), which the HBM serves from fewer channels at a time (T = 1
+// tail 44.0 -> 41.3 us; the row-major tail 40.5 us).
 template <int QS>
 __global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
     const uint16_t* __restrict__ a, int64_t sam, const uint16_t* __restrict__ w2p,
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(256) void down_tokmaj_packed_kernel(
   // token, or (u == topk) the shared expert
   auto load_piece = [&](int c, uint4 (&wr)[QS], uint4 (&ar)[QS], float& wk) {
     const int u = c >> 1;
-    const int kt0 = ((c & 1) * 4 + wv) * QS;
+    const int kt0 = ((((c & 1) * 4 + wv) + (int)(blockIdx.x >> 3)) & 7) * QS;
     const uint16_t* wb = nullptr;
     const uint16_t* arow = nullptr;
     wk = 0.f;
