@@ -241,8 +241,18 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
   uint32_t wvo = 0;  // packed: the lane's byte offset inside the item's load slot(s)
   const uint16_t* da[4];
   int da_n = 0;
+  // The first 512-k stage of the item being loaded (its stages run from there, wrapping).
+  // Plain launches: the workgroups advance in step, and with every item at the same stage
+  // the loads in flight sit a power of two apart and fall on fewer HBM channels; so each
+  // 512-row tile's 32 output slots start at their own stage (w2 at T = 4: 135.3 -> 127.3
+  // us, T = 16: 433.5 -> 421.0 us, T = 256: 1166 -> 1114 us; groups of 8, 16, 64, 128 or
+  // 256 slots measured slower).  The start depends on the output slots only, so every
+  // mapping adds an output's stages in one order.  Gated launches keep stage 0 first:
+  // there a rotation slowed w13 (T = 1: 74.4 -> 92.5 us).
+  int d_rot = 0;
   auto dma_setup = [&](int it) {
     const int L = place(it);
+    if constexpr (!GATED) d_rot = (((PAIR ? 2 : 1) * (L % num_n)) >> 5) % nks;
     const int m = L / num_n;
     const int n0 = (L % num_n) * NOC;
     const bool extra = m < xm;
@@ -331,7 +341,9 @@ __global__ __launch_bounds__(256) void moe_gemm_runs_kernel(GemmArgs p) {
       }
     }
   };
-  auto issue = [&](int s, int buf) {  // stage s (512-k run) of the item being loaded
+  auto issue = [&](int s0, int buf) {  // stage s0 (512-k run) of the item being loaded
+    int s = s0;
+    if constexpr (!GATED) s = s0 + d_rot < nks ? s0 + d_rot : s0 + d_rot - nks;
     const uint32_t sb = ring_base + (uint32_t)(buf * SE * 2);
 #pragma unroll
     for (int b = 0; b < NB; ++b)
