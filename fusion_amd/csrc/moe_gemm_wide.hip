@@ -485,6 +485,18 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     ++n_run;
     const int n0 = pid_n * NO;
     const int P = pid_n / SPLIT, sub = pid_n % SPLIT;  // the packed 512-row tile and half
+    // The item's first stage (its stages run from there, wrapping), in the 512-row tiles of
+    // the expert GEMMs (the 64- and 128-token tiles; o_proj's epilogues keep stage 0).  There most W tiles are streamed by
+    // one item, the workgroups advance in step, and with every item at the same stage the
+    // loads in flight sit a multiple of 2 MB apart; starting each expert's tiles 16 stages
+    // apart spreads them over the HBM channels (T = 2048: w13 2275 -> 2164 us, w2 1340 ->
+    // 1315 us).  The 256 x 256 tiles keep stage 0 first: there many row blocks share each
+    // W tile through L2 and the same start ran w13 4058 -> 4127 us at T = 8192.  The start
+    // depends on the expert and the 512-row tile only, so packed and in-place W, one launch
+    // or separate ones, and the atomic merge (EPI 4) add an output's stages in one order.
+    const int krot = (NTW == 512 && (EPI == 0 || EPI == 4))
+                         ? (((xs ? 0 : e) * num_n512 + P) * 16) % nk
+                         : 0;
     // the item's operands: the routed rows through the layout, the extra expert's directly
     const uint16_t* Ab = xs ? p.Ax : p.A;
     const int64_t sam = xs ? p.sax : p.sam;
@@ -552,10 +564,12 @@ __global__ __launch_bounds__(256) void moe_gemm_w512_kernel(GemmArgs p) {
     // lane reads the same 16 bytes, one cache line per instruction, into the free buffer.
     auto issue_one = [&](int i, int kt) {  // load instruction i of stage kt (clamped)
       const bool past = kt >= nk;  // wave-uniform
-      const int kc = min(kt, nk - 1) * BKS;
+      int kr = min(kt, nk - 1) + krot;  // the stage loaded, from the item's first
+      if (kr >= nk) kr -= nk;
+      const int kc = kr * BKS;
       const uint32_t sb = rb + (uint32_t)((kt % NSTAGE) * SELEM * 2);
       if (i < WI) {
-        const uint16_t* src = PACKED ? wexp + (int64_t)min(kt, nk - 1) * kPackStride : wexp + kc;
+        const uint16_t* src = PACKED ? wexp + (int64_t)kr * kPackStride : wexp + kc;
         const uint32_t vo = past ? 0u : wvoff[i];
         if (w_once)
           dma16s_nt(src, vo, sb + (uint32_t)((wvu * WI + i) * RPI * BKS * 2));
