@@ -68,7 +68,7 @@ def parse():
                     help="(internal) the process profiled for roofline.traffic: three 256 MiB "
                          "copies, then the block's w13 launch at the first --tokens value")
     ap.add_argument("--pmc-step", default="w13",
-                    choices=("w13", "w2", "block", "tail", "tail-rowmajor"),
+                    choices=("w13", "w2", "block", "tail", "tail-rowmajor", "oproj"),
                     help="(with --pmc-child) the launch profiled: the block's w13 launch, its "
                          "w2 launch, the whole block, its token-major tail (T = 1, packed "
                          "weights), or the same tail on the row-major weights")
@@ -112,6 +112,16 @@ def main() -> int:
         torch.cuda.synchronize()
         log("copy probe: 3 x 256 MiB device copies")
         del src, dst
+    if args.pmc_child and args.pmc_step == "oproj":  # o_proj + ResAdd1 alone, no expert weights
+        T = int(args.tokens.split(",")[0])
+        flush_buf = torch.empty(2 ** 28, dtype=torch.int32, device=dev)  # 1 GiB
+        step, _ = oproj_inputs(T, dev)
+        for _ in range(PMC_LAUNCHES):
+            flush_buf.zero_()
+            step()
+        torch.cuda.synchronize()
+        log(f"pmc child: T={T}, {PMC_LAUNCHES} oproj launches")
+        return 0
     t0 = time.time()
     W = expert_weights(device=dev)
     # the blocks read one resident layout, packed once here; the row-major set stays for
@@ -407,10 +417,10 @@ def hbm_traffic(T: int, timeout_s: float = 240.0) -> dict | None:
             "write_kib": w["kib_raw"], "write_scale": w["scale"], "kernel": f["kernel"]}
 
 
-def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
-    """o_proj + ResAdd1 (upstream of the block, not part of `value`): the fused chain of
-    `fusion_amd.kernels.oproj_resadd` on the reference's inputs for this T
-    (`glm52/bench/bench_f01_oproj_resadd.py:224-236`), timed like the block."""
+def oproj_inputs(T: int, dev):
+    """The fused o_proj + ResAdd1 chain of `fusion_amd.kernels.oproj_resadd` on the
+    reference's inputs for this T (`glm52/bench/bench_f01_oproj_resadd.py:224-236`): the
+    step that runs it, and K."""
     import torch
 
     from fusion_amd import roofline as RL
@@ -429,11 +439,21 @@ def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
         for fn in chain:
             fn()
 
+    return step, K
+
+
+def oproj_bench(T: int, timed, steps: int, warmup: int, dev) -> dict:
+    """o_proj + ResAdd1 (upstream of the block, not part of `value`): `oproj_inputs`'s
+    chain, timed like the block."""
+    from fusion_amd import roofline as RL
+
+    N = 6144
+    step, K = oproj_inputs(T, dev)
     ms, _ = timed(step, steps, warmup)
     us = statistics.median(ms) * 1e3
     kc = RL.oproj_cost(T, K, N)
     roof = kc.seconds() * 1e6
-    del a, b, r, out, acc32
+    del step
     return {"K": K, "us": round(us, 2), "roofline_us": round(roof, 1),
             "roofline_frac": round(roof / us, 4), "bound": kc.bound(),
             "GBps": round(kc.bytes / (us * 1e-6) / 1e9, 1),
